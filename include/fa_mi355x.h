@@ -1,0 +1,144 @@
+/*
+ * fa_mi355x.h — C ABI of the MI355X (gfx950) BF16 attention forward library
+ * (libfa_mi355x.so). Plain pointers and ints only, so ctypes, cgo, JNI or a
+ * C harness can bind it without C++ or torch types.
+ *
+ * Every entry point returns an int status: 0 (hipSuccess) or a hipError_t
+ * value. Launchers are asynchronous and stream-ordered on `stream` (a
+ * hipStream_t; NULL = the null stream); device-side failures surface on the
+ * next synchronisation, as with the reference's launchers. Launchers allocate
+ * nothing and keep no state; the caller owns q, k, v, o and the workspace.
+ *
+ * Tensors are contiguous [batch, heads, seq_len, head_dim] bf16 (IEEE
+ * binary16-brain bit patterns, 2 bytes each); accumulation is fp32; the
+ * softmax scale is 1/sqrt(head_dim) computed in float
+ * (include/flash_attention.h:21-24 of the reference).
+ *
+ * Error contract (the reference returns void and reports through
+ * cudaGetLastError; this layer returns the code directly):
+ *   FA_ERROR_UNSUPPORTED   head_dim not handled by that kernel — nothing is
+ *                          launched (the reference's launchers return silently
+ *                          here, kernels/v3/v3_tensorcore.cu:743-744);
+ *   hipErrorInvalidValue   null pointer with a non-empty shape, negative
+ *                          dimension, or a shape beyond the grid limits;
+ *   0 with no launch       any of batch, heads, seq_len equal to 0.
+ *
+ * Reference interface each symbol replaces is cited per declaration
+ * (paths relative to the RichterWang/cuda_fused_attention tree).
+ */
+#ifndef FA_MI355X_H
+#define FA_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FA_ERROR_UNSUPPORTED 801 /* == hipErrorNotSupported */
+
+/* Kernel resource report. Field meaning follows the reference's
+ * FusedTilingInfo (include/flash_attention.h:60-72); the last three fields are
+ * MI355X additions (AGPRs and the LDS/wave budgets of a gfx950 CU). */
+typedef struct fa_tiling_info {
+    int supported;
+    int block_size;                  /* threads per workgroup */
+    int tile_kv;                     /* key/value rows staged in LDS per step */
+    int rows_per_block;              /* query rows per workgroup */
+    int shared_bytes_per_block;      /* LDS bytes per workgroup */
+    int registers_per_thread;        /* VGPRs */
+    int local_bytes_per_thread;      /* scratch (spill) bytes, must be 0 */
+    int max_blocks_per_sm;           /* workgroups resident per CU */
+    int device_shared_bytes_per_sm;  /* LDS per CU */
+    int shared_limited_blocks_per_sm;
+    int agprs_per_thread;            /* accumulation VGPRs (MI355X) */
+    int waves_per_block;             /* wave64 count per workgroup (MI355X) */
+    int compute_units;               /* CUs on the current device (MI355X) */
+} fa_tiling_info;
+
+/* include/flash_attention.h:21-24 — 1.0f / sqrtf(head_dim). */
+float fa_default_scale(int head_dim);
+
+/* include/flash_attention.h:27, kernels/v0_unfused.cu:118-126 — 4*pairs*D*B*H,
+ * pairs = N^2 dense, N(N+1)/2 causal (the reference's convention). */
+double fa_attention_flops(int batch, int heads, int seq_len, int head_dim, int causal);
+
+/* include/flash_attention.h:30, kernels/v0_unfused.cu:128-131 — B*H*N*N*4. */
+size_t fa_unfused_workspace_bytes(int batch, int heads, int seq_len, int head_dim);
+
+/* include/flash_attention.h:33, kernels/v0_unfused.cu:140-155 — the unfused
+ * baseline: S = scale*Q.K^T (fp32, masked to -FLT_MAX) into `workspace`
+ * (>= fa_unfused_workspace_bytes), row softmax in place, O = bf16(P.V).
+ * Three kernels, one stream, no host sync. Any head_dim >= 1. */
+int fa_launch_attention_unfused(const void* q, const void* k, const void* v, void* o,
+                                float* workspace, int batch, int heads, int seq_len,
+                                int head_dim, int causal, void* stream);
+
+/* include/flash_attention.h:36, kernels/v0_unfused.cu:133-138 — stable row
+ * softmax in place over a [rows, cols] fp32 matrix. */
+int fa_launch_softmax_rows_inplace(float* s, int rows, int cols, void* stream);
+
+/* include/flash_attention_v0_profile.h:9-23, kernels/v0_unfused_profile.cu:121-148
+ * — the same three kernels with four hipEvent_t markers recorded on `stream`
+ * (qk_start, qk_end, softmax_end, pv_end). `events` may be NULL (no markers);
+ * otherwise it points at four hipEvent_t handles in that order. */
+int fa_launch_attention_unfused_profile(const void* q, const void* k, const void* v, void* o,
+                                        float* workspace, int batch, int heads, int seq_len,
+                                        int head_dim, int causal, void* const* events,
+                                        void* stream);
+
+/* include/flash_attention.h:90 — head_dim in {64, 128}. */
+int fa_tensorcore_v3_supported(int head_dim);
+
+/* include/flash_attention.h:92, kernels/v3/v3_tensorcore.cu:722-750 — the
+ * fused forward: QK^T and PV on gfx950 bf16 MFMA (v_mfma_f32_32x32x16_bf16),
+ * K and V^T staged in LDS, online softmax in fp32 registers, whole KV tiles
+ * above the causal diagonal skipped. */
+int fa_launch_attention_tensorcore_v3(const void* q, const void* k, const void* v, void* o,
+                                      int batch, int heads, int seq_len, int head_dim,
+                                      int causal, void* stream);
+
+/* include/flash_attention.h:94, kernels/v3/v3_tensorcore.cu:752-790 */
+int fa_query_tensorcore_v3(int head_dim, fa_tiling_info* info);
+
+/* include/flash_attention.h:96, kernels/v3/v3_tensorcore.cu:795-818 — the
+ * algorithmic HBM model of the fused kernel: Q read and O written once, K/V
+ * tiles counted once per query block that loads them (an upper bound; L2
+ * reuse brings the measured figure to Q+K+V+O once). */
+double fa_tensorcore_v3_hbm_bytes(int batch, int heads, int seq_len, int head_dim, int causal);
+
+/* include/flash_attention.h:101-107 — the reference's v3b occupancy variant.
+ * Here: the same MFMA arithmetic with 64 query rows per workgroup (twice the
+ * workgroups, for shapes that leave CUs idle at 128 rows). */
+int fa_tensorcore_v3b_supported(int head_dim);
+int fa_launch_attention_tensorcore_v3b(const void* q, const void* k, const void* v, void* o,
+                                       int batch, int heads, int seq_len, int head_dim,
+                                       int causal, void* stream);
+int fa_query_tensorcore_v3b(int head_dim, fa_tiling_info* info);
+double fa_tensorcore_v3b_hbm_bytes(int batch, int heads, int seq_len, int head_dim, int causal);
+
+/* Harness support (benchmarks/bench_flash_attention.cu:265-299): run
+ * `warmup` untimed launches of kernel `which` (0 = unfused, 1 = v3 fused,
+ * 2 = v3b fused), synchronise, then `iters` launches each bracketed by
+ * hipEventRecord on `stream`; elapsed milliseconds go to samples_ms[iters].
+ * Returns FA_ERROR_UNSUPPORTED for an unsupported head_dim and
+ * hipErrorInvalidValue for a non-positive or non-finite sample. */
+int fa_time_launches(int which, const void* q, const void* k, const void* v, void* o,
+                     float* workspace, int batch, int heads, int seq_len, int head_dim,
+                     int causal, int warmup, int iters, float* samples_ms, void* stream);
+
+/* Throughput form: `iters` back-to-back launches between one pair of events;
+ * total elapsed milliseconds in *total_ms. */
+int fa_time_batch(int which, const void* q, const void* k, const void* v, void* o,
+                  float* workspace, int batch, int heads, int seq_len, int head_dim,
+                  int causal, int iters, float* total_ms, void* stream);
+
+/* Library identification: "gfx950" and the build's kernel configuration. */
+const char* fa_build_info(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FA_MI355X_H */

@@ -1,0 +1,120 @@
+// flash_attention.h — the reference's C++ launch interface
+// (include/flash_attention.h:9-109 of RichterWang/cuda_fused_attention),
+// kept declaration-for-declaration with HIP-native types: __hip_bfloat16 for
+// __nv_bfloat16 and hipStream_t for cudaStream_t. A harness written against
+// the reference compiles against this header unchanged apart from those two
+// type names, and links libfa_mi355x.so.
+//
+// Semantics kept from the reference:
+//   * launchers return void and enqueue on `stream`; launch errors surface
+//     through hipGetLastError / the next synchronisation;
+//   * an unsupported head_dim launches nothing and returns silently;
+//   * callers own every buffer; launchers allocate nothing.
+// The kernels behind these calls are the gfx950 ones of fa_mi355x.h; the
+// reference's v1 (fused_row) and v2 (fusedtiling, v2b) study kernels are not
+// rebuilt: their queries report supported = false and their launchers are
+// no-ops, so a harness row for them prints SKIP. v3b maps to the 64-row
+// workgroup configuration of the MFMA kernel.
+#pragma once
+
+#include <hip/hip_bf16.h>
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstddef>
+
+namespace cuda_op_lab::flash_attention {
+
+struct AttentionShape
+{
+    int batch;
+    int heads;
+    int seq_len;   // query and key/value length
+    int head_dim;  // 64 or 128 for the fused kernels; any for v0
+};
+
+inline float default_scale(int head_dim)
+{
+    return 1.0f / std::sqrt(static_cast<float>(head_dim));
+}
+
+double attention_flops(const AttentionShape& shape, bool causal);
+
+size_t unfused_workspace_bytes(const AttentionShape& shape);
+
+void launch_attention_unfused(const __hip_bfloat16* q, const __hip_bfloat16* k, const __hip_bfloat16* v,
+                              __hip_bfloat16* o, float* workspace, const AttentionShape& shape, bool causal,
+                              hipStream_t stream = nullptr);
+
+void launch_softmax_rows_inplace(float* s, int rows, int cols, hipStream_t stream = nullptr);
+
+bool fused_row_supported(int head_dim);
+
+void launch_attention_fused_row(const __hip_bfloat16* q, const __hip_bfloat16* k, const __hip_bfloat16* v,
+                                __hip_bfloat16* o, const AttentionShape& shape, bool causal,
+                                hipStream_t stream = nullptr);
+
+struct FusedRowInfo
+{
+    bool supported;
+    int block_size;
+    int tile_n;
+    int shared_bytes_per_block;
+    int registers_per_thread;
+    int local_bytes_per_thread;
+    int max_blocks_per_sm;
+};
+
+FusedRowInfo query_fused_row(int head_dim);
+
+void launch_attention_fusedtiling(const __hip_bfloat16* q, const __hip_bfloat16* k, const __hip_bfloat16* v,
+                                  __hip_bfloat16* o, const AttentionShape& shape, bool causal,
+                                  hipStream_t stream = nullptr);
+
+struct FusedTilingInfo
+{
+    bool supported;
+    int block_size;
+    int tile_kv;
+    int rows_per_block;
+    int shared_bytes_per_block;
+    int registers_per_thread;
+    int local_bytes_per_thread;
+    int max_blocks_per_sm;
+    int device_shared_bytes_per_sm;
+    int shared_limited_blocks_per_sm;
+};
+
+FusedTilingInfo query_fused_tiling(int head_dim);
+
+double fused_tiling_hbm_bytes(const AttentionShape& shape, bool causal);
+
+void launch_attention_fusedtiling_v2b(const __hip_bfloat16* q, const __hip_bfloat16* k, const __hip_bfloat16* v,
+                                      __hip_bfloat16* o, const AttentionShape& shape, bool causal,
+                                      hipStream_t stream = nullptr);
+FusedTilingInfo query_fused_tiling_v2b(int head_dim);
+double fused_tiling_v2b_hbm_bytes(const AttentionShape& shape, bool causal);
+
+// The fused forward on gfx950 bf16 MFMA (the reference's tensor-core v3 slot).
+bool tensorcore_v3_supported(int head_dim);
+
+void launch_attention_tensorcore_v3(const __hip_bfloat16* q, const __hip_bfloat16* k, const __hip_bfloat16* v,
+                                    __hip_bfloat16* o, const AttentionShape& shape, bool causal,
+                                    hipStream_t stream = nullptr);
+
+FusedTilingInfo query_tensorcore_v3(int head_dim);
+
+double tensorcore_v3_hbm_bytes(const AttentionShape& shape, bool causal);
+
+// v3b slot: the same MFMA kernel with 64 query rows per workgroup.
+bool tensorcore_v3b_supported(int head_dim);
+
+void launch_attention_tensorcore_v3b(const __hip_bfloat16* q, const __hip_bfloat16* k, const __hip_bfloat16* v,
+                                     __hip_bfloat16* o, const AttentionShape& shape, bool causal,
+                                     hipStream_t stream = nullptr);
+
+FusedTilingInfo query_tensorcore_v3b(int head_dim);
+
+double tensorcore_v3b_hbm_bytes(const AttentionShape& shape, bool causal);
+
+}  // namespace cuda_op_lab::flash_attention

@@ -1,0 +1,62 @@
+"""Helpers shared by the GPU parity tests: move bf16 bit arrays to the device,
+launch a kernel through the C ABI (ctypes), read the result back. Outputs are
+prefilled with 0xFFFF (bf16 NaN) so an unwritten element fails the check
+(benchmarks/bench_flash_attention.cu:555-556)."""
+import os
+import sys
+
+import numpy as np
+
+HOST_THREADS = max(1, min(16, os.cpu_count() or 1))
+
+
+def to_dev(bits: np.ndarray):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).cuda().view(torch.bfloat16)
+
+
+def from_dev(t) -> np.ndarray:
+    import torch
+
+    return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def nan_like(t):
+    import torch
+
+    return torch.full(t.shape, -1, dtype=torch.int16, device=t.device).view(torch.bfloat16)
+
+
+def say(*parts):
+    """Name the case before a GPU step (flushed, so a fault still shows it)."""
+    print(*parts, flush=True)
+    sys.stdout.flush()
+
+
+def run(fa, kernel: str, q, k, v, causal: bool, stream=None, out=None):
+    """Launch `kernel` on device tensors and return the output tensor."""
+    import torch
+
+    shape = fa.AttentionShape(*q.shape)
+    o = nan_like(q) if out is None else out
+    st = stream if stream is not None else torch.cuda.current_stream()
+    if kernel == "v0_unfused":
+        ws = torch.empty(max(1, fa.unfused_workspace_bytes(shape) // 4), dtype=torch.float32, device=q.device)
+        assert fa.launch_attention_unfused(q, k, v, o, ws, shape, causal, stream=st)
+    elif kernel == "v3_mfma":
+        assert fa.launch_attention_tensorcore_v3(q, k, v, o, shape, causal, stream=st)
+    elif kernel == "v3b_mfma":
+        assert fa.launch_attention_tensorcore_v3b(q, k, v, o, shape, causal, stream=st)
+    else:
+        raise ValueError(kernel)
+    torch.cuda.synchronize()
+    return o
+
+
+def run_bits(fa, kernel, qb, kb, vb, causal):
+    q, k, v = to_dev(qb), to_dev(kb), to_dev(vb)
+    return from_dev(run(fa, kernel, q, k, v, causal))
+
+
+KERNELS = ["v0_unfused", "v3_mfma", "v3b_mfma"]

@@ -1,0 +1,135 @@
+"""CPU tests of libfa_mi355x.so: it loads, exports every symbol the public
+headers declare, and its host-side logic (FLOP / byte models, scale, argument
+validation that returns before any HIP call) matches the oracle and the
+reference's conventions. No kernel is launched here."""
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(REPO, "include", "fa_mi355x.h")
+
+
+def declared_c_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(fa_[a-z0-9_]+)\s*\(", text)))
+
+
+def exported_symbols(path):
+    out = subprocess.run(["nm", "-D", "--defined-only", path], check=True, capture_output=True, text=True).stdout
+    return {line.split()[-1] for line in out.splitlines() if line.strip()}
+
+
+def test_every_declared_symbol_is_exported(fa_lib):
+    declared = declared_c_symbols()
+    assert len(declared) == len(fa_lib._SIGNATURES), declared
+    exported = exported_symbols(fa_lib.LIB_PATH)
+    missing = [s for s in declared if s not in exported]
+    assert not missing, missing
+    L = fa_lib.lib()
+    for s in declared:
+        assert getattr(L, s) is not None
+
+
+def test_cpp_interface_symbols_exported(fa_lib):
+    """The C++ API of include/flash_attention.h is exported (mangled) too."""
+    out = subprocess.run(["nm", "-DC", "--defined-only", fa_lib.LIB_PATH], check=True, capture_output=True,
+                         text=True).stdout
+    for name in ("launch_attention_unfused", "launch_softmax_rows_inplace", "launch_attention_tensorcore_v3",
+                 "query_tensorcore_v3", "tensorcore_v3_hbm_bytes", "tensorcore_v3_supported", "attention_flops",
+                 "unfused_workspace_bytes", "launch_attention_unfused_profile", "launch_attention_tensorcore_v3b",
+                 "fused_row_supported", "query_fused_tiling", "launch_attention_fusedtiling_v2b"):
+        assert f"cuda_op_lab::flash_attention::{name}(" in out, name
+
+
+def test_host_models_match_oracle(fa_lib, oracle_mod):
+    L = oracle_mod.lib()
+    for (B, H, N, D) in [(1, 2, 128, 64), (2, 8, 2048, 64), (2, 8, 2048, 128), (4, 8, 8192, 128), (1, 16, 16384, 128),
+                         (1, 1, 1, 64), (3, 5, 77, 128)]:
+        shape = fa_lib.AttentionShape(B, H, N, D)
+        for causal in (False, True):
+            assert fa_lib.attention_flops(shape, causal) == oracle_mod.attention_flops(B, H, N, D, causal)
+            assert fa_lib.tensorcore_v3_hbm_bytes(shape, causal) == L.fa_oracle_blocked_kv_hbm_bytes(B, H, N, D, int(causal), 128, 64)
+            assert fa_lib.tensorcore_v3b_hbm_bytes(shape, causal) == L.fa_oracle_blocked_kv_hbm_bytes(B, H, N, D, int(causal), 64, 64)
+        assert fa_lib.unfused_workspace_bytes(shape) == L.fa_oracle_unfused_workspace_bytes(B, H, N)
+    for d in (1, 3, 64, 80, 96, 128, 256):
+        assert np.float32(fa_lib.default_scale(d)) == np.float32(oracle_mod.default_scale(d))
+
+
+def test_supported_head_dims(fa_lib):
+    for d in (64, 128):
+        assert fa_lib.tensorcore_v3_supported(d) and fa_lib.tensorcore_v3b_supported(d)
+    for d in (0, 1, 32, 63, 65, 96, 127, 129, 256):
+        assert not fa_lib.tensorcore_v3_supported(d) and not fa_lib.tensorcore_v3b_supported(d)
+
+
+def test_argument_validation_before_launch(fa_lib):
+    L = fa_lib.lib()
+    fake = 0x10000  # never dereferenced: every call below returns before a launch
+    # unsupported head_dim: nothing launched, FA_ERROR_UNSUPPORTED
+    assert L.fa_launch_attention_tensorcore_v3(fake, fake, fake, fake, 1, 1, 64, 96, 0, None) == fa_lib.FA_ERROR_UNSUPPORTED
+    assert L.fa_launch_attention_tensorcore_v3b(fake, fake, fake, fake, 1, 1, 64, 32, 1, None) == fa_lib.FA_ERROR_UNSUPPORTED
+    # empty shapes are a successful no-op
+    assert L.fa_launch_attention_tensorcore_v3(None, None, None, None, 0, 8, 64, 64, 0, None) == 0
+    assert L.fa_launch_attention_tensorcore_v3(None, None, None, None, 1, 8, 0, 128, 1, None) == 0
+    assert L.fa_launch_attention_unfused(None, None, None, None, None, 1, 0, 64, 64, 0, None) == 0
+    assert L.fa_launch_softmax_rows_inplace(None, 0, 10, None) == 0
+    # null pointers / negative dims / misaligned bases are rejected
+    assert L.fa_launch_attention_tensorcore_v3(None, fake, fake, fake, 1, 1, 64, 64, 0, None) == 1
+    assert L.fa_launch_attention_tensorcore_v3(fake, fake, fake, fake, -1, 1, 64, 64, 0, None) == 1
+    assert L.fa_launch_attention_tensorcore_v3(fake + 2, fake, fake, fake, 1, 1, 64, 64, 0, None) == 1
+    assert L.fa_launch_attention_unfused(fake, fake, fake, fake, None, 1, 1, 64, 64, 0, None) == 1
+    assert L.fa_launch_attention_unfused(fake, fake, fake, fake, fake, 1, 1, 64, 0, 0, None) == 1
+    assert L.fa_launch_softmax_rows_inplace(None, 3, 10, None) == 1
+    assert L.fa_launch_softmax_rows_inplace(fake, -1, 10, None) == 1
+    # the Python mirror: unsupported -> False (silent, like the reference), errors raise
+    shape = fa_lib.AttentionShape(1, 1, 64, 96)
+    assert fa_lib.launch_attention_tensorcore_v3(fake, fake, fake, fake, shape, False, stream=0) is False
+    with pytest.raises(fa_lib.FaError):
+        fa_lib.launch_attention_tensorcore_v3(None, fake, fake, fake, (1, 1, 64, 64), False, stream=0)
+
+
+def test_query_unsupported_needs_no_gpu(fa_lib):
+    info = fa_lib.query_tensorcore_v3(96)
+    assert info["supported"] == 0
+
+
+def test_build_info(fa_lib):
+    assert "gfx950" in fa_lib.build_info()
+
+
+def test_cpp_header_compiles_as_drop_in(tmp_path, fa_lib):
+    """A harness written against the reference interface compiles against
+    include/flash_attention.h and links libfa_mi355x.so; it runs the host-only
+    calls (no GPU needed)."""
+    src = tmp_path / "dropin.cpp"
+    src.write_text(r'''
+#include "flash_attention.h"
+#include "flash_attention_v0_profile.h"
+#include <cstdio>
+using namespace cuda_op_lab::flash_attention;
+int main() {
+    const AttentionShape shape{2, 8, 2048, 128};
+    std::printf("%.0f %zu %d %d %.9g %d\n", attention_flops(shape, false), unfused_workspace_bytes(shape),
+                (int)tensorcore_v3_supported(128), (int)fused_row_supported(64), default_scale(128),
+                (int)query_fused_tiling(64).supported);
+    void (*launch)(const __hip_bfloat16*, const __hip_bfloat16*, const __hip_bfloat16*, __hip_bfloat16*,
+                   const AttentionShape&, bool, hipStream_t) = launch_attention_tensorcore_v3;
+    return launch == nullptr;
+}
+''')
+    exe = tmp_path / "dropin"
+    hipcc = "/opt/rocm/bin/hipcc"
+    if not os.path.exists(hipcc):
+        pytest.skip("hipcc not available")
+    pkg = os.path.dirname(fa_lib.LIB_PATH)
+    subprocess.run([hipcc, "-std=c++17", "-O1", f"-I{REPO}/include", str(src), "-o", str(exe), f"-L{pkg}",
+                    "-lfa_mi355x", f"-Wl,-rpath,{pkg}"], check=True, capture_output=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split()
+    assert out[0] == "34359738368" and out[1] == str(2 * 8 * 2048 * 2048 * 4)
+    assert out[2] == "1" and out[3] == "0" and out[5] == "0"
+    assert np.float32(float(out[4])) == np.float32(1.0) / np.sqrt(np.float32(128))

@@ -1,0 +1,229 @@
+"""GPU parity of the HIP path against the FP64 oracle, through the C ABI.
+
+Gate (BASELINE + the reference's comparator, benchmarks/bench_flash_attention.cu:
+159-163,183-213): every output finite, row-scale ULP <= 2, and
+|O - O_ref| <= 2^-7 * max|O_ref row|. Both are checked by oracle.compare().
+Cases: BASELINE config 1, the reference's own accuracy shapes and inputs,
+the committed golden fixture, the boundary-N x input-family matrix of
+kernels/ablation/experiments.cu:283-295 plus the lite N set
+(benchmarks/bench_flash_attention_lite.cu:48), determinism, v3/v3b agreement,
+the v0 profile API's bitwise equality (benchmarks/profile_attention_v0.cu:98-122),
+the standalone softmax, and the error paths.
+"""
+import hashlib
+import os
+
+import numpy as np
+import pytest
+
+from gpu_common import HOST_THREADS, KERNELS, from_dev, nan_like, run, run_bits, say, to_dev
+
+pytestmark = pytest.mark.gpu
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+
+@pytest.fixture(scope="module")
+def fa(fa_lib):
+    import torch
+
+    if not torch.cuda.is_available():
+        pytest.fail("GPU tests need a visible MI355X")
+    return fa_lib
+
+
+def check(oracle, got_bits, ref, what):
+    acc = oracle.compare(got_bits, ref)
+    assert acc.passed, f"{what}: {acc}"
+    return acc
+
+
+@pytest.mark.parametrize("kernel", KERNELS)
+def test_config1_uniform_dense(fa, oracle_mod, kernel):
+    say("config1", kernel)
+    q, k, v = oracle_mod.make_inputs(1, 2, 128, 64)
+    ref = oracle_mod.attention(q, k, v, False)
+    got = run_bits(fa, kernel, q, k, v, False)
+    check(oracle_mod, got, ref, f"c1 {kernel}")
+
+
+@pytest.mark.parametrize("kernel", KERNELS)
+def test_golden_fixture(fa, oracle_mod, kernel):
+    g = np.load(os.path.join(HERE, "golden", "c1_uniform_dense.npz"))
+    B, H, N, D = (int(x) for x in g["shape"])
+    q, k, v = oracle_mod.make_inputs(B, H, N, D)
+    for name, arr in (("q", q), ("k", k), ("v", v)):
+        assert hashlib.sha256(arr.tobytes()).hexdigest() == str(g[f"sha_{name}"])
+    say("golden", kernel)
+    got = run_bits(fa, kernel, q, k, v, False)
+    check(oracle_mod, got, g["o_ref"], f"golden {kernel}")
+
+
+@pytest.mark.parametrize("kernel", KERNELS)
+@pytest.mark.parametrize("head_dim", [64, 128])
+@pytest.mark.parametrize("causal", [False, True])
+def test_reference_accuracy_shapes(fa, oracle_mod, kernel, head_dim, causal):
+    """The reference's accuracy suite: (1,2,256,D), its own mt19937 normal inputs."""
+    q, k, v = oracle_mod.make_inputs(1, 2, 256, head_dim, "normal_mt19937")
+    ref = oracle_mod.attention(q, k, v, causal)
+    say("refacc", kernel, head_dim, causal)
+    acc = check(oracle_mod, run_bits(fa, kernel, q, k, v, causal), ref, f"refacc {kernel}")
+    print(f"{kernel} D={head_dim} causal={causal} vs_double={acc.vs_double:.4e} row_scaled={acc.row_scaled:.4e} "
+          f"max_abs={acc.max_abs:.4e} ulp={acc.ulp:.2f}")
+
+
+BOUNDARY_N = [1, 7, 8, 9, 31, 32, 33, 63, 64, 65, 127, 128, 129, 256]
+FAMILIES = ["uniform", "zeros", "ones", "ramp", "scaled"]
+
+
+@pytest.mark.parametrize("family", FAMILIES)
+@pytest.mark.parametrize("kernel", KERNELS)
+def test_boundary_matrix(fa, oracle_mod, kernel, family):
+    fails = []
+    for n in BOUNDARY_N:
+        for d in (64, 128):
+            q, k, v = oracle_mod.make_inputs(1, 2, n, d, family)
+            for causal in (False, True):
+                ref = oracle_mod.attention(q, k, v, causal, threads=HOST_THREADS)
+                say("boundary", kernel, family, n, d, causal)
+                acc = oracle_mod.compare(run_bits(fa, kernel, q, k, v, causal), ref)
+                if not acc.passed:
+                    fails.append((n, d, causal, acc))
+    assert not fails, fails
+
+
+def test_multi_slab_ragged(fa, oracle_mod):
+    """Several (b,h) slabs with a partial last query block and partial KV tile."""
+    for (B, H, N, D) in [(2, 3, 200, 64), (3, 1, 333, 128), (1, 5, 65, 128)]:
+        q, k, v = oracle_mod.make_inputs(B, H, N, D, seeds={"q": 5, "k": 6, "v": 7})
+        for causal in (False, True):
+            ref = oracle_mod.attention(q, k, v, causal, threads=HOST_THREADS)
+            for kernel in KERNELS:
+                say("ragged", kernel, B, H, N, D, causal)
+                check(oracle_mod, run_bits(fa, kernel, q, k, v, causal), ref, f"ragged {kernel} {(B, H, N, D, causal)}")
+
+
+def test_v3_and_v3b_bitwise_equal(fa, oracle_mod):
+    """Each wave computes its 32 rows identically whatever the workgroup size."""
+    for (B, H, N, D) in [(1, 2, 300, 64), (2, 2, 513, 128)]:
+        q, k, v = (to_dev(x) for x in oracle_mod.make_inputs(B, H, N, D))
+        for causal in (False, True):
+            say("v3-v3b", B, H, N, D, causal)
+            a = from_dev(run(fa, "v3_mfma", q, k, v, causal))
+            b = from_dev(run(fa, "v3b_mfma", q, k, v, causal))
+            assert np.array_equal(a, b)
+
+
+def test_deterministic(fa, oracle_mod):
+    q, k, v = (to_dev(x) for x in oracle_mod.make_inputs(2, 4, 1000, 128))
+    for kernel in KERNELS:
+        for causal in (False, True):
+            say("determinism", kernel, causal)
+            a = from_dev(run(fa, kernel, q, k, v, causal))
+            b = from_dev(run(fa, kernel, q, k, v, causal))
+            assert np.array_equal(a, b)
+
+
+def test_non_default_stream(fa, oracle_mod):
+    import torch
+
+    q, k, v = oracle_mod.make_inputs(1, 2, 257, 128)
+    ref = oracle_mod.attention(q, k, v, True)
+    s = torch.cuda.Stream()
+    qd, kd, vd = to_dev(q), to_dev(k), to_dev(v)
+    torch.cuda.synchronize()
+    for kernel in KERNELS:
+        say("stream", kernel)
+        with torch.cuda.stream(s):
+            o = run(fa, kernel, qd, kd, vd, True, stream=s)
+        check(oracle_mod, from_dev(o), ref, f"stream {kernel}")
+
+
+def test_v0_profile_bitwise_equal(fa, oracle_mod):
+    """benchmarks/profile_attention_v0.cu:98-122: the instrumented launch equals
+    the plain launch bitwise, with and without events, at N in {1, 17, 256}."""
+    import torch
+
+    for n in (1, 17, 256):
+        for d in (64, 128):
+            for causal in (False, True):
+                qb, kb, vb = oracle_mod.make_inputs(1, 2, n, d, "normal_mt19937")
+                q, k, v = to_dev(qb), to_dev(kb), to_dev(vb)
+                say("v0-profile", n, d, causal)
+                plain = from_dev(run(fa, "v0_unfused", q, k, v, causal))
+                shape = fa.AttentionShape(1, 2, n, d)
+                ws = torch.empty(fa.unfused_workspace_bytes(shape) // 4, dtype=torch.float32, device="cuda")
+                events = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+                o1 = nan_like(q)
+                assert fa.launch_attention_unfused_profile(q, k, v, o1, ws, shape, causal, events=events)
+                torch.cuda.synchronize()
+                o2 = nan_like(q)
+                assert fa.launch_attention_unfused_profile(q, k, v, o2, ws, shape, causal, events=None)
+                torch.cuda.synchronize()
+                assert np.array_equal(from_dev(o1), plain) and np.array_equal(from_dev(o2), plain)
+                stages = [events[i].elapsed_time(events[i + 1]) for i in range(3)]
+                assert all(t >= 0.0 for t in stages)
+
+
+def test_softmax_rows_inplace(fa):
+    import torch
+
+    rng = np.random.default_rng(9)
+    for rows, cols in [(5, 1), (7, 3), (4, 1000), (3, 2048), (2, 8192), (2, 9000), (3, 4097)]:
+        x = rng.normal(0, 4, size=(rows, cols)).astype(np.float32)
+        x[0, : cols // 2] = -np.finfo(np.float32).max  # masked entries
+        if rows > 2:
+            x[2, :] = -np.finfo(np.float32).max        # fully masked row -> uniform
+        t = torch.from_numpy(x.copy()).cuda()
+        say("softmax", rows, cols)
+        assert fa.launch_softmax_rows_inplace(t, rows, cols)
+        torch.cuda.synchronize()
+        got = t.cpu().numpy().astype(np.float64)
+        xd = x.astype(np.float64)
+        e = np.exp(xd - xd.max(axis=1, keepdims=True))
+        want = e / e.sum(axis=1, keepdims=True)
+        np.testing.assert_allclose(got, want, rtol=2e-5, atol=1e-7)
+    # unaligned base pointer takes the scalar path
+    x = rng.normal(size=(3, 65)).astype(np.float32)
+    t = torch.from_numpy(np.concatenate([np.zeros(1, np.float32), x.reshape(-1)])).cuda()
+    assert fa.launch_softmax_rows_inplace(t.data_ptr() + 4, 3, 65)
+    torch.cuda.synchronize()
+    got = t.cpu().numpy()[1:].reshape(3, 65).astype(np.float64)
+    e = np.exp(x - x.max(axis=1, keepdims=True))
+    np.testing.assert_allclose(got, e / e.sum(axis=1, keepdims=True), rtol=2e-5, atol=1e-7)
+
+
+def test_error_paths_leave_output_untouched(fa, oracle_mod):
+    import torch
+
+    q = to_dev(oracle_mod.make_inputs(1, 1, 64, 96)[0])
+    o = nan_like(q)
+    shape = fa.AttentionShape(1, 1, 64, 96)
+    assert fa.launch_attention_tensorcore_v3(q, q, q, o, shape, False) is False
+    assert fa.launch_attention_tensorcore_v3b(q, q, q, o, shape, True) is False
+    torch.cuda.synchronize()
+    assert np.all(from_dev(o) == 0xFFFF)
+    # empty sequence: success, no launch
+    assert fa.launch_attention_tensorcore_v3(q, q, q, o, fa.AttentionShape(1, 1, 0, 64), False)
+    # misaligned base pointer is rejected on the host
+    with pytest.raises(fa.FaError):
+        fa.launch_attention_tensorcore_v3(q.data_ptr() + 2, q, q, o, fa.AttentionShape(1, 1, 16, 64), False)
+    # v0 handles any head_dim, including 96
+    qb, kb, vb = oracle_mod.make_inputs(1, 2, 50, 96)
+    ref = oracle_mod.attention(qb, kb, vb, True)
+    check(oracle_mod, run_bits(fa, "v0_unfused", qb, kb, vb, True), ref, "v0 D=96")
+    qb, kb, vb = oracle_mod.make_inputs(1, 1, 37, 5)  # odd D -> scalar load path
+    ref = oracle_mod.attention(qb, kb, vb, False)
+    check(oracle_mod, run_bits(fa, "v0_unfused", qb, kb, vb, False), ref, "v0 D=5")
+
+
+def test_query_reports_resources(fa):
+    for d in (64, 128):
+        for info in (fa.query_tensorcore_v3(d), fa.query_tensorcore_v3b(d)):
+            print(d, info)
+            assert info["supported"] == 1
+            assert info["registers_per_thread"] > 0
+            assert info["local_bytes_per_thread"] == 0, "register spill"
+            assert info["shared_bytes_per_block"] >= 2 * 2 * 64 * d * 2
+            assert info["max_blocks_per_sm"] >= 1
+            assert info["device_shared_bytes_per_sm"] >= 64 * 1024
+            assert info["compute_units"] > 0
