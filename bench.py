@@ -1,0 +1,240 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X BF16 attention forward (one GPU).
+
+Metric: BF16 attention-forward TFLOP/s and % of MI355X dense
+BF16 MFMA peak at (2,8,2048,D=64/128), dense/causal. A "step" is one fused
+forward launch over one batch of synthetic input resident in HBM. The
+headline workload is BASELINE config 2, (2,8,2048,64) dense; the other three
+(2,8,2048,D) cases, the HIP v0 baseline and its HBM roofline ride along in
+"shapes" and "v0". FLOPs follow BASELINE: 4*B*H*N^2*D, halved for causal.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+
+Prints ONE JSON line. Timing: W untimed launches, synchronize, then K
+launches bracketed by hipEvents recorded on the launch stream (inside the
+library, fa_time_batch) and by host synchronisation; `value` is the whole-job
+rate over that region, `roofline.achieved` the same FLOPs over the average
+launch duration from the events. Per-launch median/IQR (5 warmups + 30
+individually timed launches, benchmarks/bench_flash_attention.cu:265-299) is
+reported for every shape.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense BF16 MFMA (published)
+PEAK_HBM_GBPS = 8000.0      # MI355X HBM3E (published)
+METRIC = "BF16 attn fwd TFLOP/s + % MFMA peak at (2,8,2048,D=64/128) dense/causal"
+WORKLOADS = {
+    "c2": (2, 8, 2048, 64, False),
+    "c2_causal": (2, 8, 2048, 64, True),
+    "headline": (2, 8, 2048, 128, False),
+    "c3": (2, 8, 2048, 128, True),
+}
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
+
+
+def baseline_flops(B, H, N, D, causal):
+    f = 4.0 * B * H * N * N * D
+    return f / 2.0 if causal else f
+
+
+def make_device_inputs(B, H, N, D):
+    import torch
+
+    import oracle  # input generator only (seeded uniform[-1,1) bf16)
+
+    q, k, v = oracle.make_inputs(B, H, N, D, "uniform")
+    dev = [torch.from_numpy(x.view("int16")).cuda().view(torch.bfloat16) for x in (q, k, v)]
+    return (q, k, v), dev
+
+
+def measure_shape(fa, dev, B, H, N, D, causal, kernel, ws=None):
+    import torch
+
+    shape = fa.AttentionShape(B, H, N, D)
+    o = torch.empty_like(dev[0])
+    samples = fa.time_launches(kernel, *dev, o, ws, shape, causal, warmup=5, iters=30)
+    summ = fa.summarize(samples)
+    flops = baseline_flops(B, H, N, D, causal)
+    out = {
+        "median_ms": summ["median_ms"],
+        "iqr_ms": summ["iqr_ms"],
+        "tflops": flops / (summ["median_ms"] * 1e-3) / 1e12,
+    }
+    out["pct_peak"] = 100.0 * out["tflops"] / PEAK_BF16_TFLOPS
+    return out
+
+
+def cpu_baseline(host_inputs, B, H, N, D, causal):
+    """The FP64 oracle (a C++ port of benchmarks/bench_flash_attention.cu:105-145)
+    timed on this host: all rows of the workload on up to 16 threads (the GPU
+    box's CPU share), plus one slab on 1 thread (the reference's semantics)."""
+    import numpy as np
+
+    import oracle
+
+    q, k, v = host_inputs
+    threads = max(1, min(16, os.cpu_count() or 1))
+    t0 = time.perf_counter()
+    oracle.attention(q, k, v, causal, threads=threads)
+    t_all = time.perf_counter() - t0
+    flops = baseline_flops(B, H, N, D, causal)
+    rows1 = np.arange(N, dtype=np.int64)  # slab 0 only
+    t0 = time.perf_counter()
+    oracle.attention(q, k, v, causal, rows=rows1, threads=1)
+    t_one = time.perf_counter() - t0
+    return {
+        "value": flops / t_all / 1e12,
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"whole workload ({B * H * N} rows of ({B},{H},{N},{D}) {'causal' if causal else 'dense'}) "
+                  f"on {threads} threads: {t_all:.2f} s",
+        "single_thread": {"value": flops / (B * H) / t_one / 1e12, "unit": "TFLOP/s",
+                          "sample": f"slab 0 ({N} rows) on 1 thread: {t_one:.2f} s"},
+        "host_cpus": os.cpu_count(),
+    }
+
+
+def load_traffic(key):
+    try:
+        with open(TRAFFIC_FILE) as fh:
+            entry = json.load(fh).get(key)
+    except (OSError, ValueError):
+        return None
+    if not entry:
+        return None
+    return entry.get("hbm_bytes_per_launch")
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="c2")
+    ap.add_argument("--kernel", choices=["v3_mfma", "v3b_mfma"], default="v3_mfma")
+    ap.add_argument("--no-extras", action="store_true", help="only the timed region (for profiling runs)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calib-copy-mib", type=int, default=0,
+                    help="also run a plain elementwise copy of this many MiB (rocprof counter calibration)")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the attention "
+              "forward has no multi-GPU path here — run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    if args.steps <= 0 or args.warmup < 0:
+        sys.exit("steps must be > 0 and warmup >= 0")
+
+    import torch
+
+    import cuda_fused_attention_amd as fa
+
+    if not torch.cuda.is_available():
+        sys.exit("bench.py needs a GPU")
+    torch.cuda.set_device(0)
+    props = torch.cuda.get_device_properties(0)
+
+    B, H, N, D, causal = WORKLOADS[args.workload]
+    host_inputs, dev = make_device_inputs(B, H, N, D)
+    shape = fa.AttentionShape(B, H, N, D)
+    o = torch.empty_like(dev[0])
+    flops = baseline_flops(B, H, N, D, causal)
+    stream = torch.cuda.current_stream()
+
+    # warmup (untimed), then the timed region: K launches bracketed by
+    # synchronisation (wall clock) and by hipEvents on the launch stream.
+    if args.warmup:
+        fa.time_batch(args.kernel, *dev, o, None, shape, causal, iters=args.warmup, stream=stream)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    event_ms = fa.time_batch(args.kernel, *dev, o, None, shape, causal, iters=args.steps, stream=stream)
+    torch.cuda.synchronize()
+    wall_s = time.perf_counter() - t0
+
+    value = args.steps * flops / wall_s / 1e12
+    avg_launch_ms = event_ms / args.steps
+    achieved = flops / (avg_launch_ms * 1e-3) / 1e12
+
+    if args.calib_copy_mib:
+        x = torch.ones(args.calib_copy_mib * (1 << 20) // 4, dtype=torch.float32, device="cuda")
+        y = torch.empty_like(x)
+        torch.neg(x, out=y)
+        torch.cuda.synchronize()
+
+    result = {
+        "metric": METRIC,
+        "value": round(value, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": wall_s * 1e3 / args.steps,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: Q/K/V uniform[-1,1) rounded to bf16, SplitMix64 seeds 11/22/33, resident in HBM",
+        "config": {
+            "workload": f"{args.workload}: fused attention forward ({B},{H},{N},{D}) "
+                        f"{'causal' if causal else 'dense'}, [B,H,N,D] bf16, fp32 accumulate",
+            "batch": B, "heads": H, "seq_len": N, "head_dim": D, "causal": causal, "kernel": args.kernel,
+            "flops_per_step": flops, "flop_convention": "4*B*H*N^2*D, halved for causal (BASELINE)",
+        },
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(achieved, 3),
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_BF16_TFLOPS, 5),
+            "traffic": load_traffic(f"{args.kernel}:{args.workload}"),
+            "avg_launch_us": avg_launch_ms * 1e3,
+            "algorithmic_flops_per_launch": flops,
+            "min_hbm_bytes_per_launch": 8.0 * B * H * N * D,
+        },
+        "device": {"name": props.name, "compute_units": props.multi_processor_count,
+                   "gcn_arch": getattr(props, "gcnArchName", "")},
+    }
+
+    if not args.no_extras:
+        shapes = {}
+        for name, (b, h, n, d, c) in WORKLOADS.items():
+            _, sdev = make_device_inputs(b, h, n, d) if (b, h, n, d) != (B, H, N, D) else (None, dev)
+            sh = fa.AttentionShape(b, h, n, d)
+            entry = {"shape": [b, h, n, d], "causal": c}
+            for kern in ("v3_mfma", "v3b_mfma"):
+                entry[kern] = measure_shape(fa, sdev, b, h, n, d, c, kern)
+            ws = torch.empty(fa.unfused_workspace_bytes(sh) // 4, dtype=torch.float32, device="cuda")
+            v0 = measure_shape(fa, sdev, b, h, n, d, c, "v0_unfused", ws)
+            v0_bytes = 16.0 * b * h * n * n + 8.0 * b * h * n * d
+            v0["hbm_gbps"] = v0_bytes / (v0["median_ms"] * 1e-3) / 1e9
+            v0["hbm_frac"] = v0["hbm_gbps"] / PEAK_HBM_GBPS
+            v0["algorithmic_bytes"] = v0_bytes
+            v0["reference_model_bytes"] = 20.0 * b * h * n * n + 8.0 * b * h * n * d
+            entry["v0_unfused"] = v0
+            entry["speedup_vs_v0"] = v0["median_ms"] / entry["v3_mfma"]["median_ms"]
+            shapes[name] = entry
+            del ws
+        result["shapes"] = shapes
+        result["v0"] = {"bound": "hbm", "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                        "achieved": shapes[args.workload]["v0_unfused"]["hbm_gbps"],
+                        "frac": shapes[args.workload]["v0_unfused"]["hbm_frac"],
+                        "bytes_model": "16*B*H*N^2 + 8*B*H*N*D"}
+
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(host_inputs, B, H, N, D, causal)
+
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()
