@@ -115,25 +115,63 @@ __device__ __forceinline__ int swz_v(int row)
     return D == 128 ? (2 * (row & 3) + 8 * (row & 1)) : (2 * (row & 3));
 }
 
-// Issue this wave's share of one K or V tile: HBM -> LDS, no registers. The
-// source is a uniform base plus a 32-bit per-lane byte offset.
+// One 16-byte-per-lane HBM -> LDS copy: lane l's 16 bytes from
+// sbase + voff land at LDS byte address lds + 16*l (global_load_lds_dwordx4).
+// Issued through inline asm so the compiler's LDS-DMA alias tracking, which
+// cannot tell the pipeline stages apart, adds no waits of its own: every
+// consumer of the data waits on vmcnt explicitly before a barrier. M0 needs
+// one wait state between its write and the load.
+__device__ __forceinline__ void dma16(const char* sbase, uint32_t voff, uint32_t lds)
+{
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds)
+                 : "memory", "m0");
+#pragma clang diagnostic pop
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const uint16_t* p)
+{
+    return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void*)(p)));
+}
+
+// Issue this wave's share of one K or V tile (kIssues copies of 64 x 16 B):
+// block u*kWpg + wg covers rows [block*kRowsPerBlock, +kRowsPerBlock) of the
+// tile. The row and tile offsets go into the uniform scalar base; the
+// per-lane offset only holds the row within the block and the swizzled
+// chunk. Rows past the sequence end (tail tile) are clamped to the last row.
 template <int D, int kWpg, bool kIsV>
-__device__ __forceinline__ void dma_tile(const uint16_t* __restrict__ slab, int kv0, int n, uint16_t* stage, int wg,
+__device__ __forceinline__ void dma_tile(const uint16_t* __restrict__ slab, int kv0, int n, uint32_t stage_lds, int wg_s,
                                          int lane)
 {
     using C = Cfg<D, kWpg>;
-    const char* base = reinterpret_cast<const char*>(slab);
-#pragma unroll
-    for (int u = 0; u < C::kIssues; ++u)
+    constexpr int kRowsPerBlock = 64 / C::kChunks;
+    const int sub_row = lane / C::kChunks;
+    const int pchunk = lane % C::kChunks;
+    if (kv0 + kTileKV <= n)
     {
-        const int block = u * kWpg + wg;                // 64-slot block of the tile
-        const int slot = block * 64 + lane;
-        const int row = slot / C::kChunks;
-        const int pchunk = slot % C::kChunks;
-        const int lchunk = pchunk ^ (kIsV ? swz_v<D>(row) : swz_k<D>(row));
-        const int key = min(kv0 + row, n - 1);
-        const uint32_t off = static_cast<uint32_t>(key) * (D * 2) + static_cast<uint32_t>(lchunk) * 16u;
-        __builtin_amdgcn_global_load_lds(base + off, (lds_void*)(stage + block * 64 * 8), 16, 0, 0);
+#pragma unroll
+        for (int u = 0; u < C::kIssues; ++u)
+        {
+            const int block = u * kWpg + wg_s;
+            const int row0 = block * kRowsPerBlock;
+            const int lchunk = pchunk ^ (kIsV ? swz_v<D>(row0 + sub_row) : swz_k<D>(row0 + sub_row));
+            const char* sbase = reinterpret_cast<const char*>(slab) + static_cast<size_t>(kv0 + row0) * (D * 2);
+            dma16(sbase, static_cast<uint32_t>(sub_row * (D * 2) + lchunk * 16), stage_lds + block * 1024);
+        }
+    }
+    else
+    {
+#pragma unroll
+        for (int u = 0; u < C::kIssues; ++u)
+        {
+            const int block = u * kWpg + wg_s;
+            const int row = block * kRowsPerBlock + sub_row;
+            const int lchunk = pchunk ^ (kIsV ? swz_v<D>(row) : swz_k<D>(row));
+            const int key = min(kv0 + row, n - 1);
+            dma16(reinterpret_cast<const char*>(slab), static_cast<uint32_t>(key * (D * 2) + lchunk * 16),
+                  stage_lds + block * 1024);
+        }
     }
 }
 
@@ -225,10 +263,17 @@ __device__ __forceinline__ void softmax_tile(Frag<D>& f, f32x16 (&s)[2], bf16x8 
         }
     }
 
-    float mx = fmaxf(s[0][0], s[1][0]);
+    // IEEE maximum (v_maximum3_f32) needs no operand canonicalisation; the
+    // other half of the row sits in lane l^32 (v_permlane32_swap).
+    float mx = __builtin_elementwise_maximum(s[0][0], s[1][0]);
 #pragma unroll
-    for (int r = 1; r < 16; ++r) mx = fmaxf(mx, fmaxf(s[0][r], s[1][r]));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * c_log2;
+    for (int r = 1; r < 16; ++r) mx = __builtin_elementwise_maximum(mx, __builtin_elementwise_maximum(s[0][r], s[1][r]));
+    {
+        const uint32_t bits = __builtin_bit_cast(uint32_t, mx);
+        const auto swapped = __builtin_amdgcn_permlane32_swap(bits, bits, false, false);
+        mx = __builtin_elementwise_maximum(__builtin_bit_cast(float, swapped[0]), __builtin_bit_cast(float, swapped[1]));
+    }
+    mx *= c_log2;
 
     if (__any(mx > m_run + kRescaleLog2))
     {
@@ -285,6 +330,7 @@ __global__ __launch_bounds__(128 * kWpg) void fused_attention_kernel(const uint1
     const int wave = tid >> 6;
     const int grp = wave / kWpg;      // KV half
     const int wg = wave % kWpg;       // row block within the workgroup
+    const int wg_s = __builtin_amdgcn_readfirstlane(wg);  // same value, in an SGPR
     const int i = lane & 31;
     const int h = lane >> 5;
 
@@ -325,13 +371,15 @@ __global__ __launch_bounds__(128 * kWpg) void fused_attention_kernel(const uint1
         const int tb = G == 0 ? 0 : split.first1;        // first tile of this group
         const int cnt = G == 0 ? split.count0 : split.count1;
 
+        // Every DMA issue point copies a fixed number of tiles so the vmcnt
+        // waits below are constants. A tile index past the end is clamped
+        // to the last tile; such a copy lands in a stage nobody reads again.
+        auto kv_at = [&](int tile) { return min(tile, n_tiles - 1) * kTileKV; };
+
         // Prologue DMAs: V_0, K_0, K_1 of this group.
-        if (cnt > 0)
-        {
-            dma_tile<D, kWpg, true>(v_slab, tb * kTileKV, n, vb0, wg, lane);
-            dma_tile<D, kWpg, false>(k_slab, tb * kTileKV, n, kb0, wg, lane);
-        }
-        if (cnt > 1) dma_tile<D, kWpg, false>(k_slab, (tb + 1) * kTileKV, n, kb1, wg, lane);
+        dma_tile<D, kWpg, true>(v_slab, kv_at(tb), n, lds_addr(vb0), wg_s, lane);
+        dma_tile<D, kWpg, false>(k_slab, kv_at(tb), n, lds_addr(kb0), wg_s, lane);
+        dma_tile<D, kWpg, false>(k_slab, kv_at(tb + 1), n, lds_addr(kb1), wg_s, lane);
 
 #pragma unroll
         for (int ks = 0; ks < D / 16; ++ks)
@@ -383,31 +431,29 @@ __global__ __launch_bounds__(128 * kWpg) void fused_attention_kernel(const uint1
         auto valu_phase = [&](auto par_tag, int kk) {
             constexpr int kPar = decltype(par_tag)::value;
             const int t = tb + kk;
-            const bool fetch_v = kk + 1 < cnt;
-            const bool fetch_k = kk + 2 < cnt;
-            if (fetch_v) dma_tile<D, kWpg, true>(v_slab, (t + 1) * kTileKV, n, kPar ? vb0 : vb1, wg, lane);
-            if (fetch_k) dma_tile<D, kWpg, false>(k_slab, (t + 2) * kTileKV, n, kPar ? kb1 : kb0, wg, lane);
+            dma_tile<D, kWpg, true>(v_slab, kv_at(t + 1), n, lds_addr(kPar ? vb0 : vb1), wg_s, lane);
+            dma_tile<D, kWpg, false>(k_slab, kv_at(t + 2), n, lds_addr(kPar ? kb1 : kb0), wg_s, lane);
             if (t <= t_last)
-            {
                 softmax_tile<D, kCausal>(f, s, p, m_run, l_run, t * kTileKV, n, query, h, c_log2, t >= t_mask);
-            }
             // Everything but this step's DMAs must have landed.
-            if (fetch_k) wait_vm_lgkm0<2 * C::kIssues>();
-            else if (fetch_v) wait_vm_lgkm0<C::kIssues>();
-            else wait_vm_lgkm0<0>();
+            wait_vm_lgkm0<2 * C::kIssues>();
             barrier();
         };
 
         fa::fused_group_walk(cnt, mfma_phase, valu_phase);
         // Pad to the common barrier count of both groups.
         for (int b = fa::fused_group_barriers(G, cnt); b < split.barriers; ++b) barrier();
+        // Drain this wave's last (unused) copies before LDS is reused below.
+        wait_vm_lgkm0<0>();
+        barrier();
     };
 
     if (grp == 0) run_group(std::integral_constant<int, 0>{});
     else run_group(std::integral_constant<int, 1>{});
 
     // Merge: group 1 stages its (exponent base, partial sums, O^T) in LDS,
-    // group 0 folds them into its own and writes O. All DMAs have landed.
+    // group 0 folds them into its own and writes O. All DMAs have landed
+    // (every wave drained its own before the last barrier).
     float* const ostage = reinterpret_cast<float*>(wg == 0 ? k10 : wg == 1 ? k11 : wg == 2 ? v10 : v11);
     float* const ml_stage = reinterpret_cast<float*>(k00);
     if (grp == 1)

@@ -27,6 +27,8 @@ struct FusedSplit
 // Barriers group `g` executes for `count` tiles: one after the prologue DMAs,
 // one per MFMA phase (count + 1 of them: PV of the previous tile, S^T of the
 // current) and one per VALU phase (count), plus group 1's initial idle phase.
+// Both groups then pad to FusedSplit::barriers and run the same fixed tail
+// (drain, merge), so only this group-dependent part needs checking.
 FA_HD inline int fused_group_barriers(int g, int count)
 {
     return 1 + (g == 1 ? 1 : 0) + (count + 1) + count;
