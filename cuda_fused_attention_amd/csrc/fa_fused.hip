@@ -123,6 +123,16 @@ __device__ __forceinline__ int swz_v(int row)
 // one wait state between its write and the load.
 __device__ __forceinline__ void dma16(const char* sbase, uint32_t voff, uint32_t lds)
 {
+    // Both scalar operands are uniform by construction; readfirstlane makes
+    // that explicit so they are always allocated to SGPRs.
+    // readfirstlane returns int: each half goes back through uint32_t before
+    // widening, or a low word with bit 31 set would sign-extend into the
+    // high word.
+    const uint64_t base_bits = reinterpret_cast<uint64_t>(sbase);
+    const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(static_cast<uint32_t>(base_bits))));
+    const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(base_bits >> 32)));
+    sbase = reinterpret_cast<const char*>((static_cast<uint64_t>(hi) << 32) | static_cast<uint64_t>(lo));
+    lds = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(lds)));
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
     asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds)
@@ -314,16 +324,17 @@ __global__ __launch_bounds__(128 * kWpg) void fused_attention_kernel(const uint1
                                                                      float c_log2)
 {
     using C = Cfg<D, kWpg>;
-    // Per group: two K stages and two V stages, each its own LDS object so
-    // the compiler can tell a DMA into one stage from reads of another.
-    __shared__ __attribute__((aligned(16))) uint16_t k00[C::kTileElems];
-    __shared__ __attribute__((aligned(16))) uint16_t k01[C::kTileElems];
-    __shared__ __attribute__((aligned(16))) uint16_t v00[C::kTileElems];
-    __shared__ __attribute__((aligned(16))) uint16_t v01[C::kTileElems];
-    __shared__ __attribute__((aligned(16))) uint16_t k10[C::kTileElems];
-    __shared__ __attribute__((aligned(16))) uint16_t k11[C::kTileElems];
-    __shared__ __attribute__((aligned(16))) uint16_t v10[C::kTileElems];
-    __shared__ __attribute__((aligned(16))) uint16_t v11[C::kTileElems];
+    // Per group: two K stages and two V stages at compile-time offsets of one
+    // LDS array, so every operand read is a per-lane base plus an immediate.
+    __shared__ __attribute__((aligned(16))) uint16_t lds[8 * C::kTileElems];
+    uint16_t* const k00 = lds + 0 * C::kTileElems;
+    uint16_t* const k01 = lds + 1 * C::kTileElems;
+    uint16_t* const v00 = lds + 2 * C::kTileElems;
+    uint16_t* const v01 = lds + 3 * C::kTileElems;
+    uint16_t* const k10 = lds + 4 * C::kTileElems;
+    uint16_t* const k11 = lds + 5 * C::kTileElems;
+    uint16_t* const v10 = lds + 6 * C::kTileElems;
+    uint16_t* const v11 = lds + 7 * C::kTileElems;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -355,7 +366,10 @@ __global__ __launch_bounds__(128 * kWpg) void fused_attention_kernel(const uint1
     const int t_tail = (n % kTileKV) ? n / kTileKV : n_tiles;
     const int t_diag = kCausal ? (wq0 + 1) / kTileKV : n_tiles;
     const int t_mask = min(t_tail, t_diag);
-    const int t_last = kCausal ? min((wq0 + 31) / kTileKV, n_tiles - 1) : n_tiles - 1;
+    // Dense: t_last is n_tiles - 1, passed through readfirstlane so the
+    // compiler cannot fold the per-phase tests away; folded, it merges the
+    // phases' blocks and its hoisting then spills at head_dim 128.
+    const int t_last = kCausal ? min((wq0 + 31) / kTileKV, n_tiles - 1) : __builtin_amdgcn_readfirstlane(n_tiles - 1);
 
     Frag<D> f;
     const int query = wq0 + i;
