@@ -8,33 +8,39 @@
 //   * A workgroup owns 32*kWpg query rows and runs two wave groups of kWpg
 //     wave64s each. Wave w of group 0 and wave w of group 1 own the same 32
 //     rows; group 0 walks the first half of the KV tiles, group 1 the second
-//     half (split-KV inside the workgroup); their partial (max, sum, O) are
-//     merged through LDS at the end. With kWpg = 4 that is two waves per SIMD.
-//   * The groups ping-pong: phases alternate between an MFMA phase (PV of
-//     tile k-1, then S^T of tile k) and a VALU phase (online softmax of tile
-//     k), and group 1 runs one phase behind group 0. So while one wave of a
-//     SIMD feeds the matrix core the other runs exp/max/convert on the VALU.
-//     Every phase ends with a workgroup barrier; both groups execute the same
-//     number of barriers (fa_fused_schedule.hpp).
+//     half (split-KV inside the workgroup), and their partial (max, sum, O)
+//     are merged through LDS at the end. This keeps 128-row workgroups (one
+//     per CU at (2,8,2048,D)) while giving every SIMD two waves.
 //   * Both GEMMs use v_mfma_f32_32x32x16_bf16. QK^T is computed transposed,
-//     S^T = K . Q^T (K tile from LDS = A operand, the wave's Q rows in
-//     registers = B operand): lane l then holds query l % 32 and keys
-//     8*(r/4) + 4*(l/32) + r%4, so a row's max and sum need one cross-lane
-//     step. PV is computed as O^T = V^T . P^T: the exponentiated scores already
-//     are the B operand, P never leaves registers, and O^T's layout again
-//     gives lane l query l % 32, so the online-softmax rescale is per lane.
-//     The A operand (8 keys of one head dim per lane) comes from the
-//     row-major V tile through two ds_read_b64_tr_b16: within each group of
-//     16 lanes, output lane j element r is element j%4 of the 8-byte chunk
-//     addressed by source lane 4r + j/4.
-//   * K and V tiles (64 keys) are copied HBM -> LDS directly with
-//     global_load_lds_dwordx4 (lane l of an issue lands at base + 16*l), two
-//     stages per tensor per group, issued two phases before use. The LDS rows
-//     are row-major with the 16-byte chunk index XOR-swizzled per row so that
-//     every ds_read_b128 (K) and ds_read_b64_tr_b16 (V) phase hits 64 distinct
-//     banks; the swizzle is realised by choosing which global chunk each lane
-//     fetches. Rows past the sequence end are fetched from the last valid row
-//     (finite data) and masked.
+//     S^T = K . Q^T (K tile = A operand, the wave's Q rows in registers = B
+//     operand): lane l then holds query l % 32 and keys 8*(r/4) + 4*(l/32) +
+//     r%4 of a 32-key tile, so a row's max and sum need one cross-lane step
+//     (v_permlane32_swap). PV is computed as O^T = V^T . P^T: the
+//     exponentiated scores already are the B operand, P never leaves
+//     registers, and O^T's layout again gives lane l query l % 32, so the
+//     online-softmax rescale is per lane. The A operand (8 keys of one head
+//     dim per lane, in the same key order as P) comes from the row-major V
+//     tile through two ds_read_b64_tr_b16: within each group of 16 lanes,
+//     output lane j element r is element j%4 of the 8-byte chunk addressed by
+//     source lane 4r + j/4.
+//   * Software pipeline per wave, one 32-key tile per step. Step jj:
+//       block A: K operands of tile jj+1 and V operands of tile jj are read
+//                LDS -> registers; the MFMA pipe computes S^T of tile jj+1
+//                while the VALU finishes tile jj's exponentials (second half);
+//       block B: the MFMA pipe accumulates O^T += V^T P^T of tile jj while
+//                the VALU starts tile jj+1 (mask, row max, first half of the
+//                exponentials).
+//     MFMA and VALU work of one wave are independent inside each block, so
+//     the instruction stream interleaves them (sched_group_barrier) and both
+//     pipes stay busy; the second wave on the SIMD fills remaining gaps.
+//   * K and V tiles are copied HBM -> LDS directly with
+//     global_load_lds_dwordx4 (lane l of an issue lands at base + 16*l),
+//     three stages per tensor per group, issued two steps before use. The LDS
+//     rows are row-major with the 16-byte chunk index XOR-swizzled per row so
+//     that every ds_read_b128 (K) and ds_read_b64_tr_b16 (V) phase hits 64
+//     distinct banks; the swizzle is realised by choosing which global chunk
+//     each lane fetches. Rows past the sequence end are fetched from the last
+//     valid row (finite data) and masked. One workgroup barrier per step.
 //   * Scores stay in the log2 domain (scale*log2(e) folded into one FMA before
 //     v_exp_f32). The exponent base (running max) is only raised when a row's
 //     max grows by more than 2^8, then O and the row sum are rescaled; P stays
@@ -48,7 +54,6 @@
 
 #include <cmath>
 #include <cstdint>
-#include <cstdio>
 #include <type_traits>
 
 #include "fa_common.hpp"
@@ -65,22 +70,25 @@ typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
 constexpr int kTileKV = fa::kFusedTileKV;  // keys per LDS tile
+constexpr int kStages = fa::kFusedStages;  // LDS stages per tensor per group
 constexpr float kRescaleLog2 = 8.0f;       // raise the exponent base when a row max grows by > 2^8
 
 template <int D, int kWpg>
 struct Cfg
 {
-    static constexpr int kRows = 32 * kWpg;               // query rows per workgroup
-    static constexpr int kThreads = 128 * kWpg;           // two groups of kWpg waves
-    static constexpr int kChunks = D / 8;                 // 16-byte chunks per row
-    static constexpr int kTileElems = kTileKV * D;        // bf16 per K or V tile
-    static constexpr int kIssues = kTileKV * kChunks / (64 * kWpg);  // DMA issues per wave per tile
+    static constexpr int kRows = 32 * kWpg;                            // query rows per workgroup
+    static constexpr int kThreads = 128 * kWpg;                        // two groups of kWpg waves
+    static constexpr int kChunks = D / 8;                              // 16-byte chunks per row
+    static constexpr int kTileElems = kTileKV * D;                     // bf16 per K or V tile
+    static constexpr int kRowsPerIssue = 64 / kChunks;                 // rows one 64-lane DMA covers
+    static constexpr int kIssues = kTileKV / (kRowsPerIssue * kWpg);   // DMA issues per wave per tile
+    static constexpr int kGroupElems = 2 * kStages * kTileElems;       // one group's K and V stages
+    static constexpr int kLdsElems = 2 * kGroupElems;
+    static constexpr int kOStageFloats = (D / 32) * 16 * 64;           // one wave's O^T
     static_assert(D == 64 || D == 128, "head_dim 64 or 128");
-    static_assert(kIssues * 64 * kWpg == kTileKV * kChunks, "tile splits evenly over a group");
+    static_assert(kIssues * kRowsPerIssue * kWpg == kTileKV, "tile splits evenly over a group");
     static_assert(2 * kIssues < 64, "vmcnt range");
-    // the merge stages one wave's O^T (fp32) in one tile-sized LDS array
-    static_assert((D / 32) * 16 * 64 * 4 == kTileElems * 2, "O^T of a wave fills one tile array");
-    static_assert(kWpg <= 4, "merge staging uses four arrays");
+    static_assert(kWpg * (kOStageFloats + 128) * 4 <= kLdsElems * 2, "merge staging fits the LDS array");
 };
 
 // s_waitcnt with vmcnt <= N and lgkmcnt == 0 (expcnt untouched).
@@ -115,27 +123,53 @@ __device__ __forceinline__ int swz_v(int row)
     return D == 128 ? (2 * (row & 3) + 8 * (row & 1)) : (2 * (row & 3));
 }
 
-// One 16-byte-per-lane HBM -> LDS copy: lane l's 16 bytes from
-// sbase + voff land at LDS byte address lds + 16*l (global_load_lds_dwordx4).
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+// Buffer resource for raw (stride 0) byte-addressed loads: 48-bit base,
+// num_records in bytes, and the gfx9 raw-buffer configuration word. Loads at
+// offsets >= num_records return zero instead of touching memory.
+constexpr uint32_t kRawBufferConfig = 0x00020000u;
+
+// A byte address kept as two uniform 32-bit halves (scalar registers), so
+// per-tile descriptor arithmetic stays on the scalar unit.
+struct ScalarPtr
+{
+    uint32_t lo;
+    uint32_t hi;
+};
+
+__device__ __forceinline__ ScalarPtr scalar_ptr(const void* p)
+{
+    const uint64_t b = reinterpret_cast<uint64_t>(p);
+    return ScalarPtr{static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(static_cast<uint32_t>(b)))),
+                     static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(static_cast<uint32_t>(b >> 32))))};
+}
+
+// Descriptor of `bytes` bytes starting `offset` bytes after `base`.
+__device__ __forceinline__ i32x4 make_rsrc(ScalarPtr base, uint32_t offset, uint32_t bytes)
+{
+    const uint64_t b = ((static_cast<uint64_t>(base.hi) << 32) | base.lo) + offset;
+    i32x4 r;
+    r[0] = static_cast<int>(static_cast<uint32_t>(b));
+    r[1] = static_cast<int>(static_cast<uint32_t>(b >> 32) & 0xffffu);
+    r[2] = static_cast<int>(bytes);
+    r[3] = static_cast<int>(kRawBufferConfig);
+    return r;
+}
+
+// One 16-byte-per-lane HBM -> LDS copy: lane l's 16 bytes at byte offset
+// voff of the buffer land at LDS byte address lds + 16*l
+// (buffer_load_dwordx4 ... lds); offsets past the buffer's end read as zero.
 // Issued through inline asm so the compiler's LDS-DMA alias tracking, which
 // cannot tell the pipeline stages apart, adds no waits of its own: every
 // consumer of the data waits on vmcnt explicitly before a barrier. M0 needs
 // one wait state between its write and the load.
-__device__ __forceinline__ void dma16(const char* sbase, uint32_t voff, uint32_t lds)
+__device__ __forceinline__ void dma16(i32x4 rsrc, uint32_t voff, uint32_t lds)
 {
-    // Both scalar operands are uniform by construction; readfirstlane makes
-    // that explicit so they are always allocated to SGPRs.
-    // readfirstlane returns int: each half goes back through uint32_t before
-    // widening, or a low word with bit 31 set would sign-extend into the
-    // high word.
-    const uint64_t base_bits = reinterpret_cast<uint64_t>(sbase);
-    const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(static_cast<uint32_t>(base_bits))));
-    const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(base_bits >> 32)));
-    sbase = reinterpret_cast<const char*>((static_cast<uint64_t>(hi) << 32) | static_cast<uint64_t>(lo));
     lds = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(lds)));
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
-    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds)
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(rsrc), "s"(lds)
                  : "memory", "m0");
 #pragma clang diagnostic pop
 }
@@ -145,44 +179,42 @@ __device__ __forceinline__ uint32_t lds_addr(const uint16_t* p)
     return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void*)(p)));
 }
 
-// Issue this wave's share of one K or V tile (kIssues copies of 64 x 16 B):
-// block u*kWpg + wg covers rows [block*kRowsPerBlock, +kRowsPerBlock) of the
-// tile. The row and tile offsets go into the uniform scalar base; the
-// per-lane offset only holds the row within the block and the swizzled
-// chunk. Rows past the sequence end (tail tile) are clamped to the last row.
+// Per-lane byte offsets (from a tile's first row) of this wave's DMA copies
+// of one K or V tile (kIssues copies of 64 x 16 B): copy u covers tile rows
+// [row0, row0 + kRowsPerIssue) with row0 = (u*kWpg + wg) * kRowsPerIssue;
+// lane l fetches row row0 + l / kChunks, and its logical 16-byte chunk is
+// chosen so that the chunk lands at its swizzled position (the copy writes
+// lane l's 16 bytes to LDS byte 16*l of the copy's 1 KiB block).
 template <int D, int kWpg, bool kIsV>
-__device__ __forceinline__ void dma_tile(const uint16_t* __restrict__ slab, int kv0, int n, uint32_t stage_lds, int wg_s,
-                                         int lane)
+__device__ __forceinline__ void dma_lane_offsets(int wg, int lane, uint32_t (&voff)[Cfg<D, kWpg>::kIssues])
 {
     using C = Cfg<D, kWpg>;
-    constexpr int kRowsPerBlock = 64 / C::kChunks;
     const int sub_row = lane / C::kChunks;
     const int pchunk = lane % C::kChunks;
-    if (kv0 + kTileKV <= n)
-    {
 #pragma unroll
-        for (int u = 0; u < C::kIssues; ++u)
-        {
-            const int block = u * kWpg + wg_s;
-            const int row0 = block * kRowsPerBlock;
-            const int lchunk = pchunk ^ (kIsV ? swz_v<D>(row0 + sub_row) : swz_k<D>(row0 + sub_row));
-            const char* sbase = reinterpret_cast<const char*>(slab) + static_cast<size_t>(kv0 + row0) * (D * 2);
-            dma16(sbase, static_cast<uint32_t>(sub_row * (D * 2) + lchunk * 16), stage_lds + block * 1024);
-        }
-    }
-    else
+    for (int u = 0; u < C::kIssues; ++u)
     {
-#pragma unroll
-        for (int u = 0; u < C::kIssues; ++u)
-        {
-            const int block = u * kWpg + wg_s;
-            const int row = block * kRowsPerBlock + sub_row;
-            const int lchunk = pchunk ^ (kIsV ? swz_v<D>(row) : swz_k<D>(row));
-            const int key = min(kv0 + row, n - 1);
-            dma16(reinterpret_cast<const char*>(slab), static_cast<uint32_t>(key * (D * 2) + lchunk * 16),
-                  stage_lds + block * 1024);
-        }
+        const int row = (u * kWpg + wg) * C::kRowsPerIssue + sub_row;
+        const int lchunk = pchunk ^ (kIsV ? swz_v<D>(row) : swz_k<D>(row));
+        voff[u] = static_cast<uint32_t>(row * (D * 2) + lchunk * 16);
     }
+}
+
+// Buffer resource of the K or V tile starting at key kv0 (< n): it ends at
+// the slab's last row, so rows of a tail tile past the sequence end read as
+// zero (finite; their scores are masked).
+template <int D>
+__device__ __forceinline__ i32x4 tile_rsrc(ScalarPtr slab, int kv0, int n)
+{
+    return make_rsrc(slab, static_cast<uint32_t>(kv0 * (D * 2)), static_cast<uint32_t>((n - kv0) * (D * 2)));
+}
+
+// Copy u of this wave's share of one K or V tile.
+template <int D, int kWpg>
+__device__ __forceinline__ void dma_copy(i32x4 rsrc, uint32_t stage_lds, int wg_s, int u,
+                                         const uint32_t (&voff)[Cfg<D, kWpg>::kIssues])
+{
+    dma16(rsrc, voff[u], stage_lds + (u * kWpg + wg_s) * 1024);
 }
 
 template <int D>
@@ -190,94 +222,151 @@ struct Frag
 {
     bf16x8 q[D / 16];       // Q rows (B operand of S^T), whole kernel
     f32x16 o[D / 32];       // O^T accumulators
-    int k_off[D / 16];      // per-lane LDS element offsets of the K A-operand reads
-    int v_off[D / 32];      // per-lane LDS element offsets of the V tr16 reads
+    int k_off[D / 16];      // per-lane LDS byte offsets of the K A-operand reads
+    int v_off[D / 32];      // per-lane LDS byte offsets of the V tr16 reads
 };
 
 // Scheduling-group masks for __builtin_amdgcn_sched_group_barrier.
+constexpr int kSchedValu = 0x002;
 constexpr int kSchedMfma = 0x008;
 constexpr int kSchedDsRead = 0x100;
 
-// S^T (64 keys x 32 queries) = K tile . Q^T. Two operand reads run ahead of
-// the MFMA stream, then each MFMA is followed by the next read, which keeps
-// only a few operand registers in flight.
-template <int D>
-__device__ __forceinline__ void qk_tile(const uint16_t* k_stage, const Frag<D>& f, f32x16 (&s)[2])
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+// Keeps a value's producing instructions inside the current block: the empty
+// asm statement uses and redefines it, so the compiler cannot sink them past
+// the next branch (e.g. the exponentials of block A into block B, where P is
+// consumed).
+__device__ __forceinline__ void pin(float& x) { asm volatile("" : "+v"(x)); }
+__device__ __forceinline__ void pin(int& x) { asm volatile("" : "+v"(x)); }
+__device__ __forceinline__ void pin(bf16x8& x)
 {
-#pragma unroll
-    for (int b = 0; b < 2; ++b)
-    {
-        s[b] = f32x16{};
-#pragma unroll
-        for (int ks = 0; ks < D / 16; ++ks)
-        {
-            const bf16x8 a = *reinterpret_cast<const bf16x8*>(k_stage + f.k_off[ks] + b * 32 * D);
-            s[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, f.q[ks], s[b], 0, 0, 0);
-        }
-    }
-    __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
-#pragma unroll
-    for (int j = 0; j < D / 8 - 2; ++j)
-    {
-        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
-    }
-    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2, 0);
+    i32x4 bits = __builtin_bit_cast(i32x4, x);
+    asm volatile("" : "+v"(bits));
+    x = __builtin_bit_cast(bf16x8, bits);
 }
 
-// O^T += V^T . P^T for one tile (two tr16 reads per MFMA, kept two MFMAs
-// ahead).
+// K A-operands of one tile (one ds_read_b128 per MFMA).
+// The per-lane offsets are re-pinned at each use so the compiler cannot
+// hoist "offset + stage" sums out of the loop into extra registers; the
+// stage offset then folds into the ds_read immediate.
 template <int D>
-__device__ __forceinline__ void pv_tile(const uint16_t* v_stage, Frag<D>& f, const bf16x8 (&p)[4])
+__device__ __forceinline__ void load_k_ops(const uint16_t* k_stage, Frag<D>& f, bf16x8 (&ka)[D / 16])
+{
+#pragma unroll
+    for (int ks = 0; ks < D / 16; ++ks)
+    {
+        pin(f.k_off[ks]);
+        ka[ks] = *reinterpret_cast<const bf16x8*>(reinterpret_cast<const char*>(k_stage) + f.k_off[ks]);
+    }
+}
+
+// V^T A-operands of one tile (two ds_read_b64_tr_b16 per MFMA); va[db][m]
+// covers head dims 32*db.. and keys 16*m.. of the tile.
+template <int D>
+__device__ __forceinline__ void load_v_ops(const uint16_t* v_stage, Frag<D>& f, bf16x8 (&va)[D / 32][2])
 {
 #pragma unroll
     for (int db = 0; db < D / 32; ++db)
 #pragma unroll
-        for (int m = 0; m < 4; ++m)
+        for (int m = 0; m < 2; ++m)
         {
-            const uint16_t* base = v_stage + f.v_off[db] + m * 16 * D;
+            if (m == 0) pin(f.v_off[db]);
+            const uint16_t* base = reinterpret_cast<const uint16_t*>(reinterpret_cast<const char*>(v_stage) + f.v_off[db]) + m * 16 * D;
             const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(base));
             const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(base + 8 * D));
-            const bf16x8 a = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-            f.o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, p[m], f.o[db], 0, 0, 0);
+            va[db][m] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
         }
-    __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 4, 0);
-#pragma unroll
-    for (int j = 0; j < D / 8 - 2; ++j)
-    {
-        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
-    }
-    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2, 0);
 }
 
-// Online softmax of one tile's scores: s -> P (bf16, B-operand layout),
-// running max / sum updated, O rescaled when the exponent base moves.
-template <int D, bool kCausal>
-__device__ __forceinline__ void softmax_tile(Frag<D>& f, f32x16 (&s)[2], bf16x8 (&p)[4], float& m_run, float& l_run,
-                                             int kv0, int n, int query, int h, float c_log2, bool masked)
+// Compile-time loop: f(std::integral_constant<int, I>) for I in [0, N).
+template <int I, int N, class F>
+__device__ __forceinline__ void static_for(F&& f)
 {
-    if (masked)  // one code path for both cases keeps register pressure flat
+    if constexpr (I < N)
     {
-        // Key of element r of block b is kv0 + 32b + 4h + c(r) with the
-        // compile-time c(r) = 8*(r/4) + r%4; it is dead when c(r) >= limit_b.
-        // Comparing against immediates keeps 32 key indices out of registers.
-        const int first_dead = kCausal ? min(n, query + 1) : n;
-#pragma unroll
-        for (int b = 0; b < 2; ++b)
-        {
-            const int limit = first_dead - kv0 - 32 * b - 4 * h;
-#pragma unroll
-            for (int r = 0; r < 16; ++r)
-                if (8 * (r >> 2) + (r & 3) >= limit) s[b][r] = -INFINITY;
-        }
+        f(std::integral_constant<int, I>{});
+        static_for<I + 1, N>(f);
     }
+}
 
+// S^T (32 keys x 32 queries) = K tile . Q^T, MFMAs [kFirst, kFirst + kCount)
+// of the D/16 (s must be zero before the first).
+template <int D, int kFirst, int kCount>
+__device__ __forceinline__ void qk_part(const Frag<D>& f, const bf16x8 (&ka)[D / 16], f32x16& s)
+{
+#pragma unroll
+    for (int ks = kFirst; ks < kFirst + kCount; ++ks)
+        s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[ks], f.q[ks], s, 0, 0, 0);
+}
+
+// O^T += V^T . P^T for one tile, MFMAs [kFirst, kFirst + kCount) of the
+// 2*(D/32) in the order (key half m, head-dim block db): consecutive MFMAs
+// write different O blocks.
+template <int D, int kFirst, int kCount>
+__device__ __forceinline__ void pv_part(Frag<D>& f, const bf16x8 (&va)[D / 32][2], const bf16x8 (&p)[2])
+{
+#pragma unroll
+    for (int x = kFirst; x < kFirst + kCount; ++x)
+    {
+        const int m = x / (D / 32);
+        const int db = x % (D / 32);
+        f.o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[db][m], p[m], f.o[db], 0, 0, 0);
+    }
+}
+
+// Row state of the online softmax (per lane: one query, half of its keys).
+// The exponent base starts at a large finite negative value rather than
+// -inf: a row that has seen no key yet keeps it (and l = 0), and every
+// update below needs no special case (exp2 of base differences is 0 or 1
+// there, masked scores are -inf and give P = 0).
+constexpr float kEmptyBase = -1.0e30f;
+
+struct RowState
+{
+    float m = kEmptyBase;  // exponent base, log2 domain, wave-lazily raised
+    float l = 0.0f;        // partial row sum of the bf16-rounded P
+};
+
+// Exponentials of scores s[kFirst + e], e < kCount (even), against base m,
+// into p[kPos + e] (bf16); their bf16 values are added to `sum`.
+template <int kFirst, int kPos, int kCount>
+__device__ __forceinline__ void exp_part(const f32x16& s, bf16x8& p, float m, float c_log2, float& sum)
+{
+#pragma unroll
+    for (int e = 0; e < kCount; ++e)
+        p[kPos + e] = static_cast<__bf16>(__builtin_amdgcn_exp2f(fmaf(s[kFirst + e], c_log2, -m)));
+    const fa::bf16x2 ones = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
+#pragma unroll
+    for (int e = 0; e < kCount; e += 2)
+    {
+        const fa::bf16x2 pair = {p[kPos + e], p[kPos + e + 1]};
+        sum = __builtin_amdgcn_fdot2_f32_bf16(pair, ones, sum, false);
+    }
+}
+
+// Per-element mask of a tile's scores: key offset of element r is
+// 8*(r/4) + 4*(lane/32) + r%4; `limit` = first dead key offset within the
+// tile for this lane's query, minus 4*(lane/32). Comparing the compile-time
+// part against `limit` keeps 16 key indices out of VGPRs.
+__device__ __forceinline__ void mask_tile(f32x16& s, int limit)
+{
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+        if (8 * (r >> 2) + (r & 3) >= limit) s[r] = -INFINITY;
+}
+
+// Row max of a tile and the lazy base update: the base only moves when some
+// row's max exceeds it by more than 2^8 (wave-uniform decision, returned);
+// then l is scaled here and O by the caller (by `alpha`) once the MFMAs that
+// still use the old base are issued.
+__device__ __forceinline__ bool row_max_update(const f32x16& s, RowState& rs, float& alpha, float c_log2)
+{
     // IEEE maximum (v_maximum3_f32) needs no operand canonicalisation; the
     // other half of the row sits in lane l^32 (v_permlane32_swap).
-    float mx = __builtin_elementwise_maximum(s[0][0], s[1][0]);
+    float mx = __builtin_elementwise_maximum(s[0], s[1]);
 #pragma unroll
-    for (int r = 1; r < 16; ++r) mx = __builtin_elementwise_maximum(mx, __builtin_elementwise_maximum(s[0][r], s[1][r]));
+    for (int r = 2; r < 16; r += 2) mx = __builtin_elementwise_maximum(mx, __builtin_elementwise_maximum(s[r], s[r + 1]));
     {
         const uint32_t bits = __builtin_bit_cast(uint32_t, mx);
         const auto swapped = __builtin_amdgcn_permlane32_swap(bits, bits, false, false);
@@ -285,34 +374,21 @@ __device__ __forceinline__ void softmax_tile(Frag<D>& f, f32x16 (&s)[2], bf16x8 
     }
     mx *= c_log2;
 
-    if (__any(mx > m_run + kRescaleLog2))
-    {
-        const float m_new = fmaxf(m_run, mx);
-        const float alpha = (m_run == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
-        m_run = m_new;
-        l_run *= alpha;
-#pragma unroll
-        for (int db = 0; db < D / 32; ++db)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) f.o[db][r] *= alpha;
-    }
-    const float m_use = (m_run == -INFINITY) ? 0.0f : m_run;
+    const bool need = __any(mx > rs.m + kRescaleLog2);
+    const float m_new = need ? __builtin_elementwise_maximum(rs.m, mx) : rs.m;
+    alpha = __builtin_amdgcn_exp2f(rs.m - m_new);  // 1 when the base did not move
+    rs.m = m_new;
+    rs.l *= alpha;
+    return need;
+}
 
+template <int D>
+__device__ __forceinline__ void rescale_o(Frag<D>& f, float alpha)
+{
 #pragma unroll
-    for (int m = 0; m < 4; ++m)
+    for (int db = 0; db < D / 32; ++db)
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
-            p[m][e] = static_cast<__bf16>(__builtin_amdgcn_exp2f(fmaf(s[m >> 1][8 * (m & 1) + e], c_log2, -m_use)));
-
-    const fa::bf16x2 ones = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
-#pragma unroll
-    for (int m = 0; m < 4; ++m)
-#pragma unroll
-        for (int e = 0; e < 8; e += 2)
-        {
-            const fa::bf16x2 pair = {p[m][e], p[m][e + 1]};
-            l_run = __builtin_amdgcn_fdot2_f32_bf16(pair, ones, l_run, false);
-        }
+        for (int r = 0; r < 16; ++r) f.o[db][r] *= alpha;
 }
 
 template <int D, int kWpg, bool kCausal>
@@ -324,17 +400,9 @@ __global__ __launch_bounds__(128 * kWpg) void fused_attention_kernel(const uint1
                                                                      float c_log2)
 {
     using C = Cfg<D, kWpg>;
-    // Per group: two K stages and two V stages at compile-time offsets of one
+    // Group g's K stages, then its V stages, at compile-time offsets of one
     // LDS array, so every operand read is a per-lane base plus an immediate.
-    __shared__ __attribute__((aligned(16))) uint16_t lds[8 * C::kTileElems];
-    uint16_t* const k00 = lds + 0 * C::kTileElems;
-    uint16_t* const k01 = lds + 1 * C::kTileElems;
-    uint16_t* const v00 = lds + 2 * C::kTileElems;
-    uint16_t* const v01 = lds + 3 * C::kTileElems;
-    uint16_t* const k10 = lds + 4 * C::kTileElems;
-    uint16_t* const k11 = lds + 5 * C::kTileElems;
-    uint16_t* const v10 = lds + 6 * C::kTileElems;
-    uint16_t* const v11 = lds + 7 * C::kTileElems;
+    __shared__ __attribute__((aligned(16))) uint16_t lds[C::kLdsElems];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -350,12 +418,13 @@ __global__ __launch_bounds__(128 * kWpg) void fused_attention_kernel(const uint1
     const int qb_in = logical % q_blocks;
     const int qb = kCausal ? (q_blocks - 1 - qb_in) : qb_in;  // causal: heaviest first
     const int q0 = qb * C::kRows;
-    const int wq0 = q0 + 32 * wg;
+    const int wq0 = q0 + 32 * wg_s;  // uniform: the tile bounds below stay scalar
 
     const size_t slab_off = static_cast<size_t>(slab) * n * D;
     const uint16_t* q_slab = q + slab_off;
-    const uint16_t* k_slab = k + slab_off;
-    const uint16_t* v_slab = v + slab_off;
+    // K and V slab bases as uniform byte pointers (scalar registers).
+    const ScalarPtr k_bytes = scalar_ptr(k + slab_off);
+    const ScalarPtr v_bytes = scalar_ptr(v + slab_off);
 
     const int last_key = kCausal ? min(q0 + C::kRows - 1, n - 1) : n - 1;
     const int n_tiles = last_key / kTileKV + 1;
@@ -367,34 +436,43 @@ __global__ __launch_bounds__(128 * kWpg) void fused_attention_kernel(const uint1
     const int t_diag = kCausal ? (wq0 + 1) / kTileKV : n_tiles;
     const int t_mask = min(t_tail, t_diag);
     // Dense: t_last is n_tiles - 1, passed through readfirstlane so the
-    // compiler cannot fold the per-phase tests away; folded, it merges the
-    // phases' blocks and its hoisting then spills at head_dim 128.
+    // compiler cannot fold the per-step tests away; folded, it merges the
+    // step variants and its hoisting then spills at head_dim 128.
     const int t_last = kCausal ? min((wq0 + 31) / kTileKV, n_tiles - 1) : __builtin_amdgcn_readfirstlane(n_tiles - 1);
 
-    Frag<D> f;
     const int query = wq0 + i;
-    float m_run = -INFINITY;
-    float l_run = 0.0f;
+    // First key this lane's query may not see, minus 4*h (see mask_tile).
+    const int dead_base = (kCausal ? min(n, query + 1) : n) - 4 * h;
+
+    Frag<D> f;
+    RowState rs;
 
     auto run_group = [&](auto gtag) {
         constexpr int G = decltype(gtag)::value;
-        uint16_t* const kb0 = G == 0 ? k00 : k10;
-        uint16_t* const kb1 = G == 0 ? k01 : k11;
-        uint16_t* const vb0 = G == 0 ? v00 : v10;
-        uint16_t* const vb1 = G == 0 ? v01 : v11;
-        const int tb = G == 0 ? 0 : split.first1;        // first tile of this group
+        uint16_t* const kb = lds + G * C::kGroupElems;            // K stages of this group
+        uint16_t* const vb = kb + kStages * C::kTileElems;        // V stages of this group
+        const int tb = G == 0 ? 0 : split.first1;                 // first tile of this group
         const int cnt = G == 0 ? split.count0 : split.count1;
+        const int lw = min(cnt - 1, t_last - tb);                 // last local tile this wave computes
 
-        // Every DMA issue point copies a fixed number of tiles so the vmcnt
-        // waits below are constants. A tile index past the end is clamped
-        // to the last tile; such a copy lands in a stage nobody reads again.
-        auto kv_at = [&](int tile) { return min(tile, n_tiles - 1) * kTileKV; };
+        // DMA lane offsets (full tiles and the tail tile) and copy helpers.
+        // Every copy point issues a fixed number of copies so the vmcnt
+        // waits below are constants. A tile index past the end is clamped to
+        // the last tile; such a copy lands in a stage nobody reads again.
+        uint32_t koff[C::kIssues], voff[C::kIssues];
+        dma_lane_offsets<D, kWpg, false>(wg, lane, koff);
+        dma_lane_offsets<D, kWpg, true>(wg, lane, voff);
+        auto kv_at = [&](int jj) { return min(tb + jj, n_tiles - 1) * kTileKV; };
+        auto copy_k = [&](int jj, int stage, int u) {
+            dma_copy<D, kWpg>(tile_rsrc<D>(k_bytes, kv_at(jj), n), lds_addr(kb + stage * C::kTileElems), wg_s, u, koff);
+        };
+        auto copy_v = [&](int jj, int stage, int u) {
+            dma_copy<D, kWpg>(tile_rsrc<D>(v_bytes, kv_at(jj), n), lds_addr(vb + stage * C::kTileElems), wg_s, u, voff);
+        };
 
-        // Prologue DMAs: V_0, K_0, K_1 of this group.
-        dma_tile<D, kWpg, true>(v_slab, kv_at(tb), n, lds_addr(vb0), wg_s, lane);
-        dma_tile<D, kWpg, false>(k_slab, kv_at(tb), n, lds_addr(kb0), wg_s, lane);
-        dma_tile<D, kWpg, false>(k_slab, kv_at(tb + 1), n, lds_addr(kb1), wg_s, lane);
-
+        // Prologue: the wave's Q rows first, then K_0 .. K_{S-1},
+        // V_0 .. V_{S-2} of this group; S^T of tile 0 starts once Q and K_0
+        // have landed.
 #pragma unroll
         for (int ks = 0; ks < D / 16; ++ks)
         {
@@ -404,9 +482,22 @@ __global__ __launch_bounds__(128 * kWpg) void fused_attention_kernel(const uint1
                 f.q[ks] = bf16x8{};
         }
 #pragma unroll
+        for (int x = 0; x < kStages; ++x)
+#pragma unroll
+            for (int u = 0; u < C::kIssues; ++u) copy_k(x, x, u);
+#pragma unroll
+        for (int x = 0; x < kStages - 1; ++x)
+#pragma unroll
+            for (int u = 0; u < C::kIssues; ++u) copy_v(x, x, u);
+
+#pragma unroll
         for (int db = 0; db < D / 32; ++db) f.o[db] = f32x16{};
 #pragma unroll
-        for (int ks = 0; ks < D / 16; ++ks) f.k_off[ks] = i * D + (((2 * ks + h) ^ swz_k<D>(i)) << 3);
+        // Operand-read offsets carry the group's LDS base, so a read's
+        // immediate only holds the stage offset (< 64 KiB, the ds_read
+        // offset field).
+        for (int ks = 0; ks < D / 16; ++ks)
+            f.k_off[ks] = 2 * (G * C::kGroupElems + i * D + (((2 * ks + h) ^ swz_k<D>(i)) << 3));
         {
             // V tr16 source-lane role: group g16 = lane/16 -> (h = g16/2, dim
             // half g16%2); s16 = lane%16 -> row s16/4 of a 4-row group, 4-dim
@@ -419,42 +510,153 @@ __global__ __launch_bounds__(128 * kWpg) void fused_attention_kernel(const uint1
             for (int db = 0; db < D / 32; ++db)
             {
                 const int col = 32 * db + dim;
-                f.v_off[db] = vr * D + (((col >> 3) ^ swz_v<D>(vr)) << 3) + (col & 7);
+                f.v_off[db] = 2 * (G * C::kGroupElems + kStages * C::kTileElems + vr * D +
+                                   (((col >> 3) ^ swz_v<D>(vr)) << 3) + (col & 7));
             }
         }
 
+        // Q and K_0 resident (the later prologue copies may still fly).
+        wait_vm_lgkm0<(2 * kStages - 2) * C::kIssues>();
+        barrier();
+
+        // Pipeline registers: S^T and the first half of P of the current
+        // tile, double-buffered by step parity (no register copies), the
+        // second half of P, the K operands of the next tile and the V
+        // operands of the current tile.
+        f32x16 sbuf[2];
+        bf16x8 p_lo[2];
+        bf16x8 p_hi;
+        bf16x8 ka[D / 16];
+        bf16x8 va[D / 32][2];
+        if (lw >= 0)
+        {
+            load_k_ops<D>(lds, f, ka);
+            sbuf[0] = f32x16{};
+            qk_part<D, 0, D / 16>(f, ka, sbuf[0]);
+            if (tb >= t_mask) mask_tile(sbuf[0], dead_base - tb * kTileKV);
+            float alpha, sum = 0.0f;
+            (void)row_max_update(sbuf[0], rs, alpha, c_log2);  // O is still zero: no rescale
+            exp_part<0, 0, 8>(sbuf[0], p_lo[0], rs.m, c_log2, sum);
+            rs.l += sum;
+        }
         wait_vm_lgkm0<0>();
-        barrier();                          // prologue tiles resident
-        if (G == 1) barrier();              // group 1 runs one phase behind
+        barrier();  // every prologue tile resident; K_0's stage is free
+        load_k_ops<D>(lds + 1 * C::kTileElems, f, ka);  // K operands of tile 1 (used only if lw >= 1)
+        if (G == 1) barrier();  // group 1 runs half a step behind group 0
 
-        f32x16 s[2];
-        bf16x8 p[4];
+        // Each step is two blocks separated by a workgroup barrier; with
+        // group 1 half a step behind, every SIMD always has one wave in
+        // block A and one in block B, and both blocks start with their MFMA
+        // operands already in registers. A block runs in kIssues chunks:
+        // one DMA copy, then its share of the MFMAs beside its share of the
+        // VALU work (hard scheduling fences between chunks), so the copies
+        // trickle into the memory pipeline instead of stalling the wave in a
+        // burst.
+        //   Block A: V operand reads of tile jj; copies of K tile jj+4;
+        //            S^T of tile jj+1 beside the second half of tile jj's
+        //            exponentials.
+        //   Block B: K operand reads of tile jj+2; copies of V tile jj+3;
+        //            O^T += V^T P^T of tile jj beside tile jj+1's row max and
+        //            the first half of its exponentials.
+        constexpr int kChunk = C::kIssues;            // chunks per block
+        constexpr int kMfmaPer = (D / 16) / kChunk;   // MFMAs per chunk
+        constexpr int kExpPer = 8 / kChunk;           // exponentials per chunk
+        static_assert(kMfmaPer * kChunk == D / 16 && kExpPer * kChunk == 8 && kExpPer % 2 == 0, "chunking");
+        auto block_a = [&](auto par_tag, int jj) {
+            constexpr int P = decltype(par_tag)::value;
+            constexpr int B = P & 1;  // S / P register buffer of tile jj
+            __builtin_amdgcn_s_setprio(0);
+            load_v_ops<D>(lds + (P % kStages) * C::kTileElems, f, va);
+            __builtin_amdgcn_sched_barrier(0);
+            sbuf[B ^ 1] = f32x16{};
+            float sum = 0.0f;
+            static_for<0, kChunk>([&](auto ctag) {
+                constexpr int c = decltype(ctag)::value;
+                copy_k(jj + fa::kFusedKAhead, (P + fa::kFusedKAhead) % kStages, c);
+                __builtin_amdgcn_sched_barrier(0);
+                qk_part<D, c * kMfmaPer, kMfmaPer>(f, ka, sbuf[B ^ 1]);
+                exp_part<8 + c * kExpPer, c * kExpPer, kExpPer>(sbuf[B], p_hi, rs.m, c_log2, sum);
+#pragma unroll
+                for (int x = 0; x < kMfmaPer; ++x)
+                {
+                    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(kSchedValu, 8, 0);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            });
+            rs.l += sum;
+            pin(p_hi);
+            pin(rs.l);
+        };
+        auto block_b = [&](auto par_tag, int jj) {
+            constexpr int P = decltype(par_tag)::value;
+            constexpr int B = P & 1;
+            // The block-B wave (the longer block) wins issue arbitration
+            // against the block-A wave that shares its SIMD.
+            __builtin_amdgcn_s_setprio(1);
+            // Diagonal / tail tile (uniform, rare): mask before the row max.
+            // On the wave's last tile (jj == lw) the "next" S^T is a dummy
+            // product with a landed stage: masking all of it makes the head a
+            // no-op (max -inf, base unmoved, P = 0).
+            const int t_next = tb + jj + 1;
+            if (t_next >= t_mask || jj == lw)
+                mask_tile(sbuf[B ^ 1], jj == lw ? -kTileKV : dead_base - t_next * kTileKV);
+            __builtin_amdgcn_sched_barrier(0);
+            load_k_ops<D>(lds + ((P + 2) % kStages) * C::kTileElems, f, ka);
+            __builtin_amdgcn_sched_barrier(0);
+            const bf16x8 p_cur[2] = {p_lo[B], p_hi};
+            float alpha, sum = 0.0f;
+            bool moved = false;
+            static_for<0, kChunk>([&](auto ctag) {
+                constexpr int c = decltype(ctag)::value;
+                copy_v(jj + fa::kFusedVAhead, (P + fa::kFusedVAhead) % kStages, c);
+                __builtin_amdgcn_sched_barrier(0);
+                pv_part<D, c * kMfmaPer, kMfmaPer>(f, va, p_cur);
+                if constexpr (c == 0) moved = row_max_update(sbuf[B ^ 1], rs, alpha, c_log2);
+                exp_part<c * kExpPer, c * kExpPer, kExpPer>(sbuf[B ^ 1], p_lo[B ^ 1], rs.m, c_log2, sum);
+#pragma unroll
+                for (int x = 0; x < kMfmaPer; ++x)
+                {
+                    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(kSchedValu, 12, 0);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            });
+            rs.l += sum;
+            pin(p_lo[B ^ 1]);
+            pin(rs.l);
+            pin(alpha);
+            if (moved) rescale_o<D>(f, alpha);
+        };
 
-        // MFMA phase of local step kk: PV of tile kk-1 (V stage (kk-1)%2),
-        // then S^T of tile kk (K stage kk%2).
-        auto mfma_phase = [&](auto par_tag, int kk) {
-            constexpr int kPar = decltype(par_tag)::value;   // kk % 2
-            const int t_prev = tb + kk - 1;
-            if (kk >= 1 && t_prev <= t_last) pv_tile<D>(kPar ? vb0 : vb1, f, p);
-            if (kk < cnt && tb + kk <= t_last) qk_tile<D>(kPar ? kb1 : kb0, f, s);
+        // Steps this wave computes (tiles up to its diagonal / the group's
+        // end), then the group's remaining steps, in which the wave only
+        // issues its share of the copies and joins the barriers. Two loops,
+        // so the computing loop carries no idle branch.
+        const int n_active = min(cnt, lw + 1);
+        fa::fused_group_walk(n_active, [&](auto par_tag, int jj) {
+            block_a(par_tag, jj);
+            // Only the copies of steps jj-1 and jj may still be in flight:
+            // K_{jj+2} (read in block B) and V_{jj+1} (read in step jj+1)
+            // have landed and become visible.
+            wait_vm_lgkm0<3 * C::kIssues>();
+            barrier();
+            block_b(par_tag, jj);
             wait_vm_lgkm0<63>();
             barrier();
-        };
-        // VALU phase of local step kk: refill V stage (kk+1)%2 and K stage
-        // kk%2, softmax of tile kk, then wait for the previous step's DMAs.
-        auto valu_phase = [&](auto par_tag, int kk) {
-            constexpr int kPar = decltype(par_tag)::value;
-            const int t = tb + kk;
-            dma_tile<D, kWpg, true>(v_slab, kv_at(t + 1), n, lds_addr(kPar ? vb0 : vb1), wg_s, lane);
-            dma_tile<D, kWpg, false>(k_slab, kv_at(t + 2), n, lds_addr(kPar ? kb1 : kb0), wg_s, lane);
-            if (t <= t_last)
-                softmax_tile<D, kCausal>(f, s, p, m_run, l_run, t * kTileKV, n, query, h, c_log2, t >= t_mask);
-            // Everything but this step's DMAs must have landed.
-            wait_vm_lgkm0<2 * C::kIssues>();
+        });
+        for (int jj = max(n_active, 0); jj < cnt; ++jj)
+        {
+            const int stage = jj % kStages;
+#pragma unroll
+            for (int u = 0; u < C::kIssues; ++u) copy_k(jj + fa::kFusedKAhead, (stage + fa::kFusedKAhead) % kStages, u);
+            wait_vm_lgkm0<3 * C::kIssues>();
             barrier();
-        };
-
-        fa::fused_group_walk(cnt, mfma_phase, valu_phase);
+#pragma unroll
+            for (int u = 0; u < C::kIssues; ++u) copy_v(jj + fa::kFusedVAhead, (stage + fa::kFusedVAhead) % kStages, u);
+            wait_vm_lgkm0<63>();
+            barrier();
+        }
         // Pad to the common barrier count of both groups.
         for (int b = fa::fused_group_barriers(G, cnt); b < split.barriers; ++b) barrier();
         // Drain this wave's last (unused) copies before LDS is reused below.
@@ -468,28 +670,28 @@ __global__ __launch_bounds__(128 * kWpg) void fused_attention_kernel(const uint1
     // Merge: group 1 stages its (exponent base, partial sums, O^T) in LDS,
     // group 0 folds them into its own and writes O. All DMAs have landed
     // (every wave drained its own before the last barrier).
-    float* const ostage = reinterpret_cast<float*>(wg == 0 ? k10 : wg == 1 ? k11 : wg == 2 ? v10 : v11);
-    float* const ml_stage = reinterpret_cast<float*>(k00);
+    float* const ostage = reinterpret_cast<float*>(lds) + wg * C::kOStageFloats;
+    float* const ml_stage = reinterpret_cast<float*>(lds) + kWpg * C::kOStageFloats + wg * 128;
     if (grp == 1)
     {
 #pragma unroll
         for (int db = 0; db < D / 32; ++db)
 #pragma unroll
             for (int r = 0; r < 16; ++r) ostage[(db * 16 + r) * 64 + lane] = f.o[db][r];
-        ml_stage[wg * 128 + lane] = m_run;
-        ml_stage[wg * 128 + 64 + lane] = l_run;
+        ml_stage[lane] = rs.m;
+        ml_stage[64 + lane] = rs.l;
     }
     wait_vm_lgkm0<0>();
     barrier();
     if (grp == 1) return;
 
     {
-        const float m1 = ml_stage[wg * 128 + lane];
-        const float l1 = ml_stage[wg * 128 + 64 + lane];
-        const float m = fmaxf(m_run, m1);
-        const float a0 = (m_run == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m_run - m);
-        const float a1 = (m1 == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m1 - m);
-        l_run = l_run * a0 + l1 * a1;
+        const float m1 = ml_stage[lane];
+        const float l1 = ml_stage[64 + lane];
+        const float m = __builtin_elementwise_maximum(rs.m, m1);
+        const float a0 = __builtin_amdgcn_exp2f(rs.m - m);
+        const float a1 = __builtin_amdgcn_exp2f(m1 - m);
+        rs.l = rs.l * a0 + l1 * a1;
 #pragma unroll
         for (int db = 0; db < D / 32; ++db)
 #pragma unroll
@@ -497,21 +699,35 @@ __global__ __launch_bounds__(128 * kWpg) void fused_attention_kernel(const uint1
     }
 
     // Epilogue: the two lane halves hold partial row sums of the same query.
-    const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+    // O^T (lane = query) is transposed through this wave's own staging area
+    // (nothing else reads it any more) into row-major bf16 with XOR-swizzled
+    // 16-byte chunks, then stored as contiguous 16-byte pieces: the wave's
+    // 32 rows are one contiguous block of O.
+    const float l_tot = rs.l + __shfl_xor(rs.l, 32, 64);
     const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-    if (query < n)
+    constexpr int kRowChunks = D / 8;
+    uint16_t* const obuf = reinterpret_cast<uint16_t*>(ostage);
+#pragma unroll
+    for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+        {
+            uint2 packed;
+            packed.x = fa::pack_bf16x2(f.o[db][4 * g + 0] * inv, f.o[db][4 * g + 1] * inv);
+            packed.y = fa::pack_bf16x2(f.o[db][4 * g + 2] * inv, f.o[db][4 * g + 3] * inv);
+            const int chunk = (4 * db + g) ^ (i & (kRowChunks - 1));
+            *reinterpret_cast<uint2*>(obuf + i * D + chunk * 8 + 4 * h) = packed;
+        }
+    wait_vm_lgkm0<63>();
+#pragma unroll
+    for (int u = 0; u < D / 16; ++u)
     {
-        uint16_t* o_row = o + slab_off + static_cast<size_t>(query) * D;
-#pragma unroll
-        for (int db = 0; db < D / 32; ++db)
-#pragma unroll
-            for (int g = 0; g < 4; ++g)
-            {
-                uint2 packed;
-                packed.x = fa::pack_bf16x2(f.o[db][4 * g + 0] * inv, f.o[db][4 * g + 1] * inv);
-                packed.y = fa::pack_bf16x2(f.o[db][4 * g + 2] * inv, f.o[db][4 * g + 3] * inv);
-                *reinterpret_cast<uint2*>(o_row + 32 * db + 8 * g + 4 * h) = packed;
-            }
+        const int x = u * 64 + lane;
+        const int row = x / kRowChunks;
+        const int c = x % kRowChunks;
+        const uint4 chunk = *reinterpret_cast<const uint4*>(obuf + row * D + ((c ^ (row & (kRowChunks - 1))) * 8));
+        if (wq0 + row < n)
+            *reinterpret_cast<uint4*>(o + slab_off + static_cast<size_t>(wq0 + row) * D + c * 8) = chunk;
     }
 }
 

@@ -1,7 +1,8 @@
-// Phase / barrier schedule of the fused kernel's two wave groups, shared by
-// the device code and a host-side checker (tests compile this header with a
-// plain C++ compiler and verify that both groups always execute the same
-// number of workgroup barriers).
+// Tile / stage / barrier schedule of the fused kernel's two wave groups,
+// shared by the device code and a host-side checker (tests compile this
+// header with a plain C++ compiler and replay the walk: both groups must
+// execute the same number of workgroup barriers, every LDS stage must be
+// free when a DMA is issued into it and landed before it is read).
 #pragma once
 
 #include <type_traits>
@@ -14,7 +15,20 @@
 
 namespace fa {
 
-constexpr int kFusedTileKV = 64;
+constexpr int kFusedTileKV = 32;  // keys per LDS tile
+constexpr int kFusedStages = 4;   // LDS stages per tensor (K, V) per wave group
+
+// Pipeline of one group, local step jj (tile jj of the group):
+//   block A  read the V operands of tile jj (LDS -> registers); DMA K tile
+//            jj + kFusedKAhead (its copies spread between the MFMAs);
+//   mid      wait until only the DMAs of steps jj-1 and jj are in flight;
+//            barrier;
+//   block B  read the K operands of tile jj + 2; DMA V tile jj + kFusedVAhead;
+//   end      wait for the LDS reads; barrier.
+// The prologue copies K_0 .. K_3 and V_0 .. V_2 and reads the K operands of
+// tiles 0 and 1 itself.
+constexpr int kFusedKAhead = kFusedStages;      // into K_jj's stage (read in step jj - 2)
+constexpr int kFusedVAhead = kFusedStages - 1;  // into V_{jj-1}'s stage (read in step jj - 1)
 
 struct FusedSplit
 {
@@ -25,33 +39,33 @@ struct FusedSplit
 };
 
 // Barriers group `g` executes for `count` tiles: one after the prologue DMAs,
-// one per MFMA phase (count + 1 of them: PV of the previous tile, S^T of the
-// current) and one per VALU phase (count), plus group 1's initial idle phase.
-// Both groups then pad to FusedSplit::barriers and run the same fixed tail
-// (drain, merge), so only this group-dependent part needs checking.
-FA_HD inline int fused_group_barriers(int g, int count)
-{
-    return 1 + (g == 1 ? 1 : 0) + (count + 1) + count;
-}
+// one after the prologue's first S tile, group 1's idle half step (it runs
+// half a step behind group 0), and two per step (mid and end). Both groups
+// then pad to FusedSplit::barriers and run the same fixed tail (drain, merge).
+FA_HD inline int fused_group_barriers(int g, int count) { return 2 + (g == 1 ? 1 : 0) + 2 * count; }
 
-// The phase walk of one group over its `count` tiles: MFMA phase 0, then
-// (VALU phase kk, MFMA phase kk+1) for kk = 0 .. count-1. Each callback runs
-// exactly one workgroup barrier; the first argument is kk % 2 as a
-// compile-time std::integral_constant (the LDS stage parity).
-template <class MfmaPhase, class ValuPhase>
-FA_HD inline void fused_group_walk(int count, MfmaPhase&& mfma_phase, ValuPhase&& valu_phase)
+// The step walk of one group over its `count` tiles: step(kk, jj) for
+// jj = 0 .. count-1 with kk = jj % kFusedUnroll as a compile-time
+// std::integral_constant: kk % kFusedStages is the LDS stage rotation and
+// kk % 2 the register double buffer of S and P. Each step runs exactly two
+// workgroup barriers.
+constexpr int kFusedUnroll = kFusedStages;
+static_assert(kFusedUnroll % 2 == 0, "the S / P double buffer needs an even unroll");
+
+template <class Step>
+FA_HD inline void fused_group_walk(int count, Step&& step)
 {
-    int kk = 0;
-    for (;;)
+    int jj = 0;
+    while (jj < count)
     {
-        mfma_phase(std::integral_constant<int, 0>{}, kk);
-        if (kk >= count) break;
-        valu_phase(std::integral_constant<int, 0>{}, kk);
-        ++kk;
-        mfma_phase(std::integral_constant<int, 1>{}, kk);
-        if (kk >= count) break;
-        valu_phase(std::integral_constant<int, 1>{}, kk);
-        ++kk;
+        step(std::integral_constant<int, 0>{}, jj);
+        if (++jj >= count) break;
+        step(std::integral_constant<int, 1>{}, jj);
+        if (++jj >= count) break;
+        step(std::integral_constant<int, 2>{}, jj);
+        if (++jj >= count) break;
+        step(std::integral_constant<int, 3>{}, jj);
+        ++jj;
     }
 }
 

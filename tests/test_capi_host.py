@@ -53,8 +53,8 @@ def test_host_models_match_oracle(fa_lib, oracle_mod):
         shape = fa_lib.AttentionShape(B, H, N, D)
         for causal in (False, True):
             assert fa_lib.attention_flops(shape, causal) == oracle_mod.attention_flops(B, H, N, D, causal)
-            assert fa_lib.tensorcore_v3_hbm_bytes(shape, causal) == L.fa_oracle_blocked_kv_hbm_bytes(B, H, N, D, int(causal), 128, 64)
-            assert fa_lib.tensorcore_v3b_hbm_bytes(shape, causal) == L.fa_oracle_blocked_kv_hbm_bytes(B, H, N, D, int(causal), 64, 64)
+            assert fa_lib.tensorcore_v3_hbm_bytes(shape, causal) == L.fa_oracle_blocked_kv_hbm_bytes(B, H, N, D, int(causal), 128, 32)
+            assert fa_lib.tensorcore_v3b_hbm_bytes(shape, causal) == L.fa_oracle_blocked_kv_hbm_bytes(B, H, N, D, int(causal), 64, 32)
         assert fa_lib.unfused_workspace_bytes(shape) == L.fa_oracle_unfused_workspace_bytes(B, H, N)
     for d in (1, 3, 64, 80, 96, 128, 256):
         assert np.float32(fa_lib.default_scale(d)) == np.float32(oracle_mod.default_scale(d))

@@ -1,17 +1,21 @@
-"""CPU check of the fused kernel's barrier schedule (csrc/fa_fused_schedule.hpp).
+"""CPU check of the fused kernel's tile / stage / barrier schedule
+(csrc/fa_fused_schedule.hpp).
 
 The kernel's two wave groups must execute exactly the same number of
-workgroup barriers or the workgroup deadlocks. The header holds the phase walk
-the kernel itself runs (fused_group_walk); this test compiles that header with
-g++, drives the walk with counting callbacks, and checks for every tile count
-that (a) the walk performs fused_group_barriers() barriers, (b) the stage
-parity argument equals kk % 2, and (c) after padding both groups reach the
-same total, split.barriers.
+workgroup barriers or the workgroup deadlocks, and the LDS stage rotation must
+never overwrite a tile that a later step still reads. The header holds the
+walk the kernel itself runs (fused_group_walk) and the pipeline distances; this
+test compiles it with g++, replays the walk with a model of the kernel's
+per-step actions and checks, for every tile count:
+  (a) the walk performs fused_group_barriers() barriers and the compile-time
+      step argument equals jj % kFusedUnroll;
+  (b) both groups reach the same total, split.barriers, after padding;
+  (c) every K / V stage is read only after the DMA that filled it was waited
+      for and a barrier passed, and no DMA targets a stage whose tile is still
+      to be read (so every read sees the tile it expects).
 """
 import os
 import subprocess
-
-import pytest
 
 REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 CSRC = os.path.join(REPO, "cuda_fused_attention_amd", "csrc")
@@ -19,21 +23,81 @@ CSRC = os.path.join(REPO, "cuda_fused_attention_amd", "csrc")
 PROGRAM = r'''
 #include "fa_fused_schedule.hpp"
 #include <cstdio>
+#include <vector>
+using namespace fa;
+constexpr int S = kFusedStages;
+
+// A stage's state: which tile it holds, when its copy was issued (epoch =
+// barriers passed at issue time, plus the step-local order) and whether the
+// wave has waited for it.
+struct Stage { int tile = -1; int issue_seq = -1; bool landed = false; int landed_epoch = -1; };
+
+long bad = 0;
+int epoch = 0;      // workgroup barriers passed
+int seq = 0;        // copy issue sequence number
+std::vector<Stage> ks, vs;
+
+// Copy `tile` into stage `st`; the stage's previous tile must have been
+// consumed: its last read happened in a step that already ended with a
+// barrier (`consumed` = highest tile of that tensor whose reads are done).
+void dma(std::vector<Stage>& arr, int st, int tile, int consumed) {
+    if (arr[st].tile >= 0 && arr[st].tile > consumed) ++bad;
+    arr[st] = Stage{tile, seq++, false, -1};
+}
+// vmcnt-style wait: every copy issued before `keep_from_seq` has landed.
+void wait_before(int keep_from_seq) {
+    for (auto* a : {&ks, &vs})
+        for (auto& s : *a)
+            if (!s.landed && s.issue_seq >= 0 && s.issue_seq < keep_from_seq) { s.landed = true; s.landed_epoch = epoch; }
+}
+void barrier() { ++epoch; }
+// A read needs the expected tile, landed before the most recent barrier.
+void read(std::vector<Stage>& arr, int st, int tile) {
+    if (arr[st].tile != tile || !arr[st].landed || arr[st].landed_epoch >= epoch) ++bad;
+}
+
 int main() {
-    long bad = 0;
-    for (int n_tiles = 1; n_tiles <= 20000; ++n_tiles) {
-        const fa::FusedSplit sp = fa::fused_split(n_tiles);
+    for (int n_tiles = 1; n_tiles <= 3000; ++n_tiles) {
+        const FusedSplit sp = fused_split(n_tiles);
         if (sp.count0 + sp.count1 != n_tiles || sp.count0 < sp.count1 || sp.first1 != sp.count0) ++bad;
         for (int g = 0; g < 2; ++g) {
             const int cnt = g == 0 ? sp.count0 : sp.count1;
-            int barriers = 1 + (g == 1 ? 1 : 0);   // prologue, group 1's idle phase
-            int mfma = 0, valu = 0;
-            fa::fused_group_walk(cnt,
-                [&](auto par, int kk) { ++barriers; ++mfma; if (decltype(par)::value != kk % 2 || kk > cnt) ++bad; },
-                [&](auto par, int kk) { ++barriers; ++valu; if (decltype(par)::value != kk % 2 || kk >= cnt) ++bad; });
-            if (mfma != cnt + 1 || valu != cnt) ++bad;
-            if (barriers != fa::fused_group_barriers(g, cnt)) ++bad;
-            if (barriers > sp.barriers) ++bad;       // padding cannot be negative
+            ks.assign(S, Stage{}); vs.assign(S, Stage{}); epoch = 0; seq = 0;
+            // prologue: K_0..K_{S-1}, V_0..V_{S-2}; wait for K_0; barrier
+            for (int x = 0; x < S; ++x) dma(ks, x, x, -1);
+            const int after_k0 = 1;  // copies issued after K_0 may fly
+            for (int x = 0; x < S - 1; ++x) dma(vs, x, x, -1);
+            wait_before(after_k0);
+            barrier();
+            int barriers = 1;
+            if (cnt > 0) read(ks, 0, 0);                 // S^T of tile 0
+            wait_before(seq); barrier(); ++barriers;     // all prologue copies landed
+            if (cnt > 1) read(ks, 1 % S, 1);             // K operands of tile 1
+            if (g == 1) { barrier(); ++barriers; }       // half-step offset
+            int k_consumed = 1, v_consumed = -1;
+            int prev_first_seq = seq;                    // first copy of step jj-1
+            int steps = 0;
+            fused_group_walk(cnt, [&](auto par, int jj) {
+                ++steps;
+                if (decltype(par)::value != jj % kFusedUnroll) ++bad;
+                // block A: V operands of tile jj; copies of K tile jj+KAhead
+                read(vs, jj % S, jj);
+                const int step_first_seq = seq;
+                dma(ks, (jj + kFusedKAhead) % S, jj + kFusedKAhead, k_consumed);
+                // mid: only copies of steps jj-1 and jj may fly
+                wait_before(prev_first_seq);
+                barrier(); ++barriers;
+                // block B: K operands of tile jj+2; copies of V tile jj+VAhead
+                if (jj + 2 < cnt) read(ks, (jj + 2) % S, jj + 2);
+                dma(vs, (jj + kFusedVAhead) % S, jj + kFusedVAhead, v_consumed);
+                barrier(); ++barriers;                   // end: LDS reads done
+                v_consumed = jj;
+                k_consumed = jj + 2;
+                prev_first_seq = step_first_seq;
+            });
+            if (steps != cnt) ++bad;
+            if (barriers != fused_group_barriers(g, cnt)) ++bad;
+            if (barriers > sp.barriers) ++bad;
         }
     }
     std::printf("%ld\n", bad);
@@ -42,11 +106,35 @@ int main() {
 '''
 
 
-def test_barrier_schedule_matches_for_both_groups(tmp_path):
+def test_schedule_barriers_and_stages(tmp_path):
     src = tmp_path / "sched.cpp"
     src.write_text(PROGRAM)
     exe = tmp_path / "sched"
-    r = subprocess.run(["g++", "-std=c++17", "-O1", f"-I{CSRC}", str(src), "-o", str(exe)], capture_output=True, text=True)
+    r = subprocess.run(["g++", "-std=c++17", "-O1", f"-I{CSRC}", str(src), "-o", str(exe)], capture_output=True,
+                       text=True)
     assert r.returncode == 0, r.stderr
     out = subprocess.run([str(exe)], capture_output=True, text=True)
     assert out.returncode == 0 and out.stdout.strip() == "0", out.stdout + out.stderr
+
+
+def test_schedule_checker_catches_a_short_pipeline(tmp_path):
+    """Planted mistakes: a K prefetch two tiles further ahead overwrites a
+    stage still to be read, and a mid-step wait that lets one more step of
+    copies fly reads a stage before its copy landed; the checker must report
+    both."""
+    plants = [
+        ("dma(ks, (jj + kFusedKAhead) % S, jj + kFusedKAhead, k_consumed);",
+         "dma(ks, (jj + kFusedKAhead + 2) % S, jj + kFusedKAhead + 2, k_consumed);"),
+        ("prev_first_seq = step_first_seq;", "prev_first_seq = jj > 0 ? prev_first_seq : step_first_seq;"),
+    ]
+    for i, (old, new) in enumerate(plants):
+        assert old in PROGRAM
+        src = tmp_path / f"sched_bad{i}.cpp"
+        src.write_text(PROGRAM.replace(old, new))
+        exe = tmp_path / f"sched_bad{i}"
+        r = subprocess.run(["g++", "-std=c++17", "-O1", f"-I{CSRC}", str(src), "-o", str(exe)], capture_output=True,
+                           text=True)
+        assert r.returncode == 0, r.stderr
+        out = subprocess.run([str(exe)], capture_output=True, text=True)
+        assert out.returncode != 0 and out.stdout.strip() != "0", (i, out.stdout)
+

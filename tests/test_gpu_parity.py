@@ -102,15 +102,31 @@ def test_multi_slab_ragged(fa, oracle_mod):
                 check(oracle_mod, run_bits(fa, kernel, q, k, v, causal), ref, f"ragged {kernel} {(B, H, N, D, causal)}")
 
 
-def test_v3_and_v3b_bitwise_equal(fa, oracle_mod):
-    """Each wave computes its 32 rows identically whatever the workgroup size."""
+def test_v3_and_v3b_agree(fa, oracle_mod):
+    """Dense: each wave computes its 32 rows identically whatever the workgroup
+    size (both configurations split the same KV range the same way), so the
+    outputs are bitwise equal. Causal: the KV range a workgroup walks ends at
+    its own last row, so the 128-row and 64-row configurations split it
+    between their two wave groups at different tiles and sum in a different
+    order; both must pass the oracle gate and agree to one bf16 ulp of the
+    row scale."""
     for (B, H, N, D) in [(1, 2, 300, 64), (2, 2, 513, 128)]:
-        q, k, v = (to_dev(x) for x in oracle_mod.make_inputs(B, H, N, D))
+        qb, kb, vb = oracle_mod.make_inputs(B, H, N, D)
+        q, k, v = to_dev(qb), to_dev(kb), to_dev(vb)
         for causal in (False, True):
             say("v3-v3b", B, H, N, D, causal)
             a = from_dev(run(fa, "v3_mfma", q, k, v, causal))
             b = from_dev(run(fa, "v3b_mfma", q, k, v, causal))
-            assert np.array_equal(a, b)
+            if not causal:
+                assert np.array_equal(a, b)
+                continue
+            ref = oracle_mod.attention(qb, kb, vb, True, threads=HOST_THREADS)
+            check(oracle_mod, a, ref, "v3 causal")
+            check(oracle_mod, b, ref, "v3b causal")
+            af = oracle_mod.bf16_to_f32(a).astype(np.float64).reshape(-1, D)
+            bf = oracle_mod.bf16_to_f32(b).astype(np.float64).reshape(-1, D)
+            row_scale = np.abs(ref.reshape(-1, D)).max(axis=1, keepdims=True)
+            assert np.all(np.abs(af - bf) <= 2.0 ** -7 * row_scale)
 
 
 def test_deterministic(fa, oracle_mod):
@@ -223,7 +239,7 @@ def test_query_reports_resources(fa):
             assert info["supported"] == 1
             assert info["registers_per_thread"] > 0
             assert info["local_bytes_per_thread"] == 0, "register spill"
-            assert info["shared_bytes_per_block"] >= 2 * 2 * 64 * d * 2
+            assert info["shared_bytes_per_block"] >= 2 * 2 * 32 * d * 2
             assert info["max_blocks_per_sm"] >= 1
             assert info["device_shared_bytes_per_sm"] >= 64 * 1024
             assert info["compute_units"] > 0
