@@ -10,13 +10,18 @@ headline workload is BASELINE config 2, (2,8,2048,64) dense; the other three
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
 
-Prints ONE JSON line. Timing: W untimed launches, synchronize, then K
-launches bracketed by hipEvents recorded on the launch stream (inside the
-library, fa_time_batch) and by host synchronisation; `value` is the whole-job
+Prints ONE JSON line. Order: the per-shape extras (median/IQR of 5 warmups +
+30 individually timed launches per kernel, benchmarks/bench_flash_attention.cu:265-299,
+for the four (2,8,2048,D) cases and the v0 baseline), then a clock ramp
+(untimed launches of the measured kernel for --ramp-s seconds: the GPU's
+clock takes a few hundred milliseconds of load to settle, and a cold start
+reads up to 10 % slow), then W untimed warmup launches, a synchronisation, and
+K launches bracketed by hipEvents recorded on the launch stream (inside the
+library, fa_time_batch) and by host synchronisation. `value` is the whole-job
 rate over that region, `roofline.achieved` the same FLOPs over the average
-launch duration from the events. Per-launch median/IQR (5 warmups + 30
-individually timed launches, benchmarks/bench_flash_attention.cu:265-299) is
-reported for every shape.
+launch duration from the events. Inputs come from the package's seeded
+generator (cuda_fused_attention_amd/inputs.py); only the cpu_baseline leg
+loads the oracle.
 """
 from __future__ import annotations
 
@@ -47,13 +52,10 @@ def baseline_flops(B, H, N, D, causal):
 
 
 def make_device_inputs(B, H, N, D):
-    import torch
+    from cuda_fused_attention_amd import inputs
 
-    import oracle  # input generator only (seeded uniform[-1,1) bf16)
-
-    q, k, v = oracle.make_inputs(B, H, N, D, "uniform")
-    dev = [torch.from_numpy(x.view("int16")).cuda().view(torch.bfloat16) for x in (q, k, v)]
-    return (q, k, v), dev
+    host = inputs.make_uniform_inputs(B, H, N, D)
+    return host, [inputs.to_device(x) for x in host]
 
 
 def measure_shape(fa, dev, B, H, N, D, causal, kernel, ws=None):
@@ -118,10 +120,12 @@ def load_traffic(key):
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--ramp-s", type=float, default=0.3, help="seconds of untimed launches before the warmup")
     ap.add_argument("--workload", choices=sorted(WORKLOADS), default="c2")
-    ap.add_argument("--kernel", choices=["v3_mfma", "v3b_mfma"], default="v3_mfma")
+    ap.add_argument("--kernel", choices=["v3_mfma", "v3b_mfma", "v0_unfused"], default="v3_mfma",
+                    help="kernel in the timed region (v0_unfused: the three-kernel baseline, HBM roofline)")
     ap.add_argument("--no-extras", action="store_true", help="only the timed region (for profiling runs)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
@@ -150,14 +154,45 @@ def main():
     o = torch.empty_like(dev[0])
     flops = baseline_flops(B, H, N, D, causal)
     stream = torch.cuda.current_stream()
+    timed_ws = None
+    if args.kernel == "v0_unfused":
+        timed_ws = torch.empty(fa.unfused_workspace_bytes(shape) // 4, dtype=torch.float32, device="cuda")
 
-    # warmup (untimed), then the timed region: K launches bracketed by
-    # synchronisation (wall clock) and by hipEvents on the launch stream.
+    shapes = None
+    if not args.no_extras:
+        shapes = {}
+        for name, (b, h, n, d, c) in WORKLOADS.items():
+            _, sdev = make_device_inputs(b, h, n, d) if (b, h, n, d) != (B, H, N, D) else (None, dev)
+            sh = fa.AttentionShape(b, h, n, d)
+            entry = {"shape": [b, h, n, d], "causal": c}
+            for kern in ("v3_mfma", "v3b_mfma"):
+                entry[kern] = measure_shape(fa, sdev, b, h, n, d, c, kern)
+            ws = torch.empty(fa.unfused_workspace_bytes(sh) // 4, dtype=torch.float32, device="cuda")
+            v0 = measure_shape(fa, sdev, b, h, n, d, c, "v0_unfused", ws)
+            v0_bytes = 16.0 * b * h * n * n + 8.0 * b * h * n * d
+            v0["hbm_gbps"] = v0_bytes / (v0["median_ms"] * 1e-3) / 1e9
+            v0["hbm_frac"] = v0["hbm_gbps"] / PEAK_HBM_GBPS
+            v0["algorithmic_bytes"] = v0_bytes
+            v0["reference_model_bytes"] = 20.0 * b * h * n * n + 8.0 * b * h * n * d
+            entry["v0_unfused"] = v0
+            entry["speedup_vs_v0"] = v0["median_ms"] / entry["v3_mfma"]["median_ms"]
+            shapes[name] = entry
+            del ws, sdev
+        torch.cuda.synchronize()
+
+    # Clock ramp: untimed launches until --ramp-s seconds have passed.
+    ramp_launches = 0
+    t_ramp = time.perf_counter()
+    while time.perf_counter() - t_ramp < args.ramp_s:
+        fa.time_batch(args.kernel, *dev, o, timed_ws, shape, causal, iters=50, stream=stream)
+        ramp_launches += 50
+    # W untimed warmup launches, then the timed region: K launches bracketed
+    # by synchronisation (wall clock) and by hipEvents on the launch stream.
     if args.warmup:
-        fa.time_batch(args.kernel, *dev, o, None, shape, causal, iters=args.warmup, stream=stream)
+        fa.time_batch(args.kernel, *dev, o, timed_ws, shape, causal, iters=args.warmup, stream=stream)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    event_ms = fa.time_batch(args.kernel, *dev, o, None, shape, causal, iters=args.steps, stream=stream)
+    event_ms = fa.time_batch(args.kernel, *dev, o, timed_ws, shape, causal, iters=args.steps, stream=stream)
     torch.cuda.synchronize()
     wall_s = time.perf_counter() - t0
 
@@ -205,25 +240,16 @@ def main():
                    "gcn_arch": getattr(props, "gcnArchName", "")},
     }
 
-    if not args.no_extras:
-        shapes = {}
-        for name, (b, h, n, d, c) in WORKLOADS.items():
-            _, sdev = make_device_inputs(b, h, n, d) if (b, h, n, d) != (B, H, N, D) else (None, dev)
-            sh = fa.AttentionShape(b, h, n, d)
-            entry = {"shape": [b, h, n, d], "causal": c}
-            for kern in ("v3_mfma", "v3b_mfma"):
-                entry[kern] = measure_shape(fa, sdev, b, h, n, d, c, kern)
-            ws = torch.empty(fa.unfused_workspace_bytes(sh) // 4, dtype=torch.float32, device="cuda")
-            v0 = measure_shape(fa, sdev, b, h, n, d, c, "v0_unfused", ws)
-            v0_bytes = 16.0 * b * h * n * n + 8.0 * b * h * n * d
-            v0["hbm_gbps"] = v0_bytes / (v0["median_ms"] * 1e-3) / 1e9
-            v0["hbm_frac"] = v0["hbm_gbps"] / PEAK_HBM_GBPS
-            v0["algorithmic_bytes"] = v0_bytes
-            v0["reference_model_bytes"] = 20.0 * b * h * n * n + 8.0 * b * h * n * d
-            entry["v0_unfused"] = v0
-            entry["speedup_vs_v0"] = v0["median_ms"] / entry["v3_mfma"]["median_ms"]
-            shapes[name] = entry
-            del ws
+    if args.kernel == "v0_unfused":
+        # The baseline is bounded by HBM: algorithmic bytes = S written once,
+        # read and written once by the softmax, read once by PV, plus Q,K,V,O.
+        v0_bytes = 16.0 * B * H * N * N + 8.0 * B * H * N * D
+        gbps = v0_bytes / (avg_launch_ms * 1e-3) / 1e9
+        result["roofline"].update({"bound": "hbm", "achieved": round(gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                                   "frac": round(gbps / PEAK_HBM_GBPS, 5), "algorithmic_bytes_per_launch": v0_bytes,
+                                   "bytes_model": "16*B*H*N^2 + 8*B*H*N*D (three kernels per launch)"})
+    result["clock_ramp_launches"] = ramp_launches
+    if shapes is not None:
         result["shapes"] = shapes
         result["v0"] = {"bound": "hbm", "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                         "achieved": shapes[args.workload]["v0_unfused"]["hbm_gbps"],

@@ -24,23 +24,32 @@
 //     output lane j element r is element j%4 of the 8-byte chunk addressed by
 //     source lane 4r + j/4.
 //   * Software pipeline per wave, one 32-key tile per step. Step jj:
-//       block A: K operands of tile jj+1 and V operands of tile jj are read
-//                LDS -> registers; the MFMA pipe computes S^T of tile jj+1
-//                while the VALU finishes tile jj's exponentials (second half);
-//       block B: the MFMA pipe accumulates O^T += V^T P^T of tile jj while
-//                the VALU starts tile jj+1 (mask, row max, first half of the
-//                exponentials).
+//       block A: the V operands of tile jj are read LDS -> registers; the
+//                MFMA pipe computes S^T of tile jj+1 (its K operands were
+//                read in the previous block B) while the VALU finishes tile
+//                jj's exponentials (second half); the wave issues its share
+//                of the DMA copies of K tile jj+4;
+//       mid:     wait until only the copies of steps jj-1 and jj are in
+//                flight, workgroup barrier;
+//       block B: the K operands of tile jj+2 are read; the MFMA pipe
+//                accumulates O^T += V^T P^T of tile jj while the VALU starts
+//                tile jj+1 (mask, row max, first half of the exponentials);
+//                the wave issues its share of the copies of V tile jj+3;
+//       end:     wait for the LDS reads, workgroup barrier.
 //     MFMA and VALU work of one wave are independent inside each block, so
-//     the instruction stream interleaves them (sched_group_barrier) and both
-//     pipes stay busy; the second wave on the SIMD fills remaining gaps.
-//   * K and V tiles are copied HBM -> LDS directly with
-//     global_load_lds_dwordx4 (lane l of an issue lands at base + 16*l),
-//     three stages per tensor per group, issued two steps before use. The LDS
-//     rows are row-major with the 16-byte chunk index XOR-swizzled per row so
-//     that every ds_read_b128 (K) and ds_read_b64_tr_b16 (V) phase hits 64
-//     distinct banks; the swizzle is realised by choosing which global chunk
-//     each lane fetches. Rows past the sequence end are fetched from the last
-//     valid row (finite data) and masked. One workgroup barrier per step.
+//     the instruction stream interleaves them (sched_group_barrier), with one
+//     DMA issue between consecutive MFMA chunks; the wave of the other group
+//     on the same SIMD runs half a step behind and fills the remaining gaps
+//     (s_setprio gives the block-B wave issue priority).
+//   * K and V tiles go HBM -> LDS directly with buffer_load_dwordx4 ... lds
+//     (lane l of an issue lands at M0 + 16*l), four stages per tensor per
+//     group. The LDS rows are row-major with the 16-byte chunk index
+//     XOR-swizzled per row so that every ds_read_b128 (K) and
+//     ds_read_b64_tr_b16 (V) phase hits distinct banks; the swizzle is
+//     realised by choosing which global chunk each lane fetches. The buffer
+//     descriptor of a tile ends at the slab's last row, so rows past the
+//     sequence end read as zero (and are masked). Descriptor arithmetic is
+//     scalar: slab bases and tile indices are wave-uniform.
 //   * Scores stay in the log2 domain (scale*log2(e) folded into one FMA before
 //     v_exp_f32). The exponent base (running max) is only raised when a row's
 //     max grows by more than 2^8, then O and the row sum are rescaled; P stays

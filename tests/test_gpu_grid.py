@@ -10,7 +10,8 @@ tile, which hold the sequence start, the partial tail and the longest causal
 rows, plus 32 seeded random rows per slab).
 
 Stress: (1,16,16384,128) causal with Q, K ~ N(0, 3^2) so logits exceed 50 and
-the online-softmax rescale is exercised; V uniform. Sampled rows as above.
+the online-softmax rescale is exercised; V uniform. Sampled rows as above,
+plus the 64 rows of head 0 whose visible logits are largest (|s| > 50).
 """
 import numpy as np
 import pytest
@@ -68,13 +69,30 @@ def test_grid_tolerance(fa, oracle_mod, B, D):
     assert not fails, fails
 
 
+def causal_row_max_logit(qf, kf, scale, chunk=2048):
+    """max over visible keys of |scale * q.k| for every query row of one slab
+    (float32 products of the bf16 inputs; an input property, not a result)."""
+    n = qf.shape[0]
+    out = np.empty(n, dtype=np.float32)
+    cols = np.arange(n)[None, :]
+    for r0 in range(0, n, chunk):
+        s = np.abs(qf[r0:r0 + chunk] @ kf.T)
+        s = np.where(cols <= np.arange(r0, r0 + chunk)[:, None], s, 0.0)
+        out[r0:r0 + chunk] = s.max(axis=1) * scale
+    return out
+
+
 def test_long_sequence_stress(fa, oracle_mod):
     B, H, N, D = 1, 16, 16384, 128
     qb, kb, vb = oracle_mod.make_inputs(B, H, N, D, "stress")
-    qf = oracle_mod.bf16_to_f32(qb[0, 0, :64]).astype(np.float64)
-    kf = oracle_mod.bf16_to_f32(kb[0, 0, :64]).astype(np.float64)
-    assert np.abs(qf @ kf.T).max() * oracle_mod.default_scale(D) > 50  # logits really exceed 50
-    rows = oracle_mod.sample_rows(B, H, N, rows_per_slab=32, tile=64, seed=5)
+    # Logits reach |s| > 50 (logit std ~9 at sigma 3, D 128): find head 0's
+    # rows with the largest logits and put the 64 largest into the checked
+    # sample, next to the stratified rows of every head.
+    row_max = causal_row_max_logit(oracle_mod.bf16_to_f32(qb[0, 0]), oracle_mod.bf16_to_f32(kb[0, 0]),
+                                   oracle_mod.default_scale(D))
+    assert row_max.max() > 50, row_max.max()
+    extreme = np.argsort(row_max)[-64:]
+    rows = np.union1d(oracle_mod.sample_rows(B, H, N, rows_per_slab=32, tile=64, seed=5), extreme).astype(np.int64)
     ref = oracle_mod.attention(qb, kb, vb, True, rows=rows, threads=HOST_THREADS)
     q, k, v = to_dev(qb), to_dev(kb), to_dev(vb)
     for kernel in KERNELS:
