@@ -259,11 +259,11 @@ __device__ __forceinline__ void pin(bf16x8& x)
 // The per-lane offsets are re-pinned at each use so the compiler cannot
 // hoist "offset + stage" sums out of the loop into extra registers; the
 // stage offset then folds into the ds_read immediate.
-template <int D>
+template <int D, int kFirst = 0, int kCount = D / 16>
 __device__ __forceinline__ void load_k_ops(const uint16_t* k_stage, Frag<D>& f, bf16x8 (&ka)[D / 16])
 {
 #pragma unroll
-    for (int ks = 0; ks < D / 16; ++ks)
+    for (int ks = kFirst; ks < kFirst + kCount; ++ks)
     {
         pin(f.k_off[ks]);
         ka[ks] = *reinterpret_cast<const bf16x8*>(reinterpret_cast<const char*>(k_stage) + f.k_off[ks]);
@@ -272,11 +272,11 @@ __device__ __forceinline__ void load_k_ops(const uint16_t* k_stage, Frag<D>& f, 
 
 // V^T A-operands of one tile (two ds_read_b64_tr_b16 per MFMA); va[db][m]
 // covers head dims 32*db.. and keys 16*m.. of the tile.
-template <int D>
+template <int D, int kFirst = 0, int kCount = D / 32>
 __device__ __forceinline__ void load_v_ops(const uint16_t* v_stage, Frag<D>& f, bf16x8 (&va)[D / 32][2])
 {
 #pragma unroll
-    for (int db = 0; db < D / 32; ++db)
+    for (int db = kFirst; db < kFirst + kCount; ++db)
 #pragma unroll
         for (int m = 0; m < 2; ++m)
         {
@@ -369,20 +369,23 @@ __device__ __forceinline__ void mask_tile(f32x16& s, int limit)
 // row's max exceeds it by more than 2^8 (wave-uniform decision, returned);
 // then l is scaled here and O by the caller (by `alpha`) once the MFMAs that
 // still use the old base are issued.
-__device__ __forceinline__ bool row_max_update(const f32x16& s, RowState& rs, float& alpha, float c_log2)
+// Row max of a tile's scores in the log2 domain (scaled by c_log2). IEEE
+// maximum (v_maximum3_f32) needs no operand canonicalisation; the other half
+// of the row sits in lane l^32 (v_permlane32_swap).
+__device__ __forceinline__ float row_max_log2(const f32x16& s, float c_log2)
 {
-    // IEEE maximum (v_maximum3_f32) needs no operand canonicalisation; the
-    // other half of the row sits in lane l^32 (v_permlane32_swap).
     float mx = __builtin_elementwise_maximum(s[0], s[1]);
 #pragma unroll
     for (int r = 2; r < 16; r += 2) mx = __builtin_elementwise_maximum(mx, __builtin_elementwise_maximum(s[r], s[r + 1]));
-    {
-        const uint32_t bits = __builtin_bit_cast(uint32_t, mx);
-        const auto swapped = __builtin_amdgcn_permlane32_swap(bits, bits, false, false);
-        mx = __builtin_elementwise_maximum(__builtin_bit_cast(float, swapped[0]), __builtin_bit_cast(float, swapped[1]));
-    }
-    mx *= c_log2;
+    const uint32_t bits = __builtin_bit_cast(uint32_t, mx);
+    const auto swapped = __builtin_amdgcn_permlane32_swap(bits, bits, false, false);
+    mx = __builtin_elementwise_maximum(__builtin_bit_cast(float, swapped[0]), __builtin_bit_cast(float, swapped[1]));
+    return mx * c_log2;
+}
 
+__device__ __forceinline__ bool row_max_update(const f32x16& s, RowState& rs, float& alpha, float c_log2)
+{
+    const float mx = row_max_log2(s, c_log2);
     const bool need = __any(mx > rs.m + kRescaleLog2);
     const float m_new = need ? __builtin_elementwise_maximum(rs.m, mx) : rs.m;
     alpha = __builtin_amdgcn_exp2f(rs.m - m_new);  // 1 when the base did not move
@@ -481,7 +484,9 @@ __global__ __launch_bounds__(128 * kWpg) void fused_attention_kernel(const uint1
 
         // Prologue: the wave's Q rows first, then K_0 .. K_{S-1},
         // V_0 .. V_{S-2} of this group; S^T of tile 0 starts once Q and K_0
-        // have landed.
+        // have landed. Step 0 waits for every prologue copy: the workgroups
+        // of a slab then start their walks together and keep reading the
+        // same tiles at about the same time, which the L2 serves best.
 #pragma unroll
         for (int ks = 0; ks < D / 16; ++ks)
         {
@@ -556,9 +561,11 @@ __global__ __launch_bounds__(128 * kWpg) void fused_attention_kernel(const uint1
         // Each step is two blocks separated by a workgroup barrier; with
         // group 1 half a step behind, every SIMD always has one wave in
         // block A and one in block B, and both blocks start with their MFMA
-        // operands already in registers. A block runs in kIssues chunks:
-        // one DMA copy, then its share of the MFMAs beside its share of the
-        // VALU work (hard scheduling fences between chunks), so the copies
+        // operands already in registers. A block runs in kIssues chunks
+        // (hard scheduling fences between chunks): the chunk's first MFMA,
+        // one DMA copy, then the rest of its MFMAs beside its share of the
+        // operand reads for the other block and of the VALU work, so the
+        // matrix pipe starts at the top of every chunk and the copies
         // trickle into the memory pipeline instead of stalling the wave in a
         // burst.
         //   Block A: V operand reads of tile jj; copies of K tile jj+4;
@@ -570,24 +577,29 @@ __global__ __launch_bounds__(128 * kWpg) void fused_attention_kernel(const uint1
         constexpr int kChunk = C::kIssues;            // chunks per block
         constexpr int kMfmaPer = (D / 16) / kChunk;   // MFMAs per chunk
         constexpr int kExpPer = 8 / kChunk;           // exponentials per chunk
+        constexpr int kVPer = (D / 32) / kChunk;      // V operand blocks read per chunk
+        constexpr int kKPer = (D / 16) / kChunk;      // K operands read per chunk
         static_assert(kMfmaPer * kChunk == D / 16 && kExpPer * kChunk == 8 && kExpPer % 2 == 0, "chunking");
+        static_assert(kVPer * kChunk == D / 32 && kKPer * kChunk == D / 16 && kMfmaPer >= 2, "chunking");
         auto block_a = [&](auto par_tag, int jj) {
             constexpr int P = decltype(par_tag)::value;
             constexpr int B = P & 1;  // S / P register buffer of tile jj
             __builtin_amdgcn_s_setprio(0);
-            load_v_ops<D>(lds + (P % kStages) * C::kTileElems, f, va);
-            __builtin_amdgcn_sched_barrier(0);
             sbuf[B ^ 1] = f32x16{};
             float sum = 0.0f;
             static_for<0, kChunk>([&](auto ctag) {
                 constexpr int c = decltype(ctag)::value;
+                qk_part<D, c * kMfmaPer, 1>(f, ka, sbuf[B ^ 1]);
+                __builtin_amdgcn_sched_barrier(0);
                 copy_k(jj + fa::kFusedKAhead, (P + fa::kFusedKAhead) % kStages, c);
                 __builtin_amdgcn_sched_barrier(0);
-                qk_part<D, c * kMfmaPer, kMfmaPer>(f, ka, sbuf[B ^ 1]);
+                load_v_ops<D, c * kVPer, kVPer>(lds + (P % kStages) * C::kTileElems, f, va);
+                qk_part<D, c * kMfmaPer + 1, kMfmaPer - 1>(f, ka, sbuf[B ^ 1]);
                 exp_part<8 + c * kExpPer, c * kExpPer, kExpPer>(sbuf[B], p_hi, rs.m, c_log2, sum);
 #pragma unroll
-                for (int x = 0; x < kMfmaPer; ++x)
+                for (int x = 1; x < kMfmaPer; ++x)
                 {
+                    __builtin_amdgcn_sched_group_barrier(kSchedDsRead, (4 * kVPer + kMfmaPer - 2) / (kMfmaPer - 1), 0);
                     __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
                     __builtin_amdgcn_sched_group_barrier(kSchedValu, 8, 0);
                 }
@@ -611,23 +623,25 @@ __global__ __launch_bounds__(128 * kWpg) void fused_attention_kernel(const uint1
             if (t_next >= t_mask || jj == lw)
                 mask_tile(sbuf[B ^ 1], jj == lw ? -kTileKV : dead_base - t_next * kTileKV);
             __builtin_amdgcn_sched_barrier(0);
-            load_k_ops<D>(lds + ((P + 2) % kStages) * C::kTileElems, f, ka);
-            __builtin_amdgcn_sched_barrier(0);
             const bf16x8 p_cur[2] = {p_lo[B], p_hi};
             float alpha, sum = 0.0f;
             bool moved = false;
             static_for<0, kChunk>([&](auto ctag) {
                 constexpr int c = decltype(ctag)::value;
+                pv_part<D, c * kMfmaPer, 1>(f, va, p_cur);
+                __builtin_amdgcn_sched_barrier(0);
                 copy_v(jj + fa::kFusedVAhead, (P + fa::kFusedVAhead) % kStages, c);
                 __builtin_amdgcn_sched_barrier(0);
-                pv_part<D, c * kMfmaPer, kMfmaPer>(f, va, p_cur);
+                load_k_ops<D, c * kKPer, kKPer>(lds + ((P + 2) % kStages) * C::kTileElems, f, ka);
+                pv_part<D, c * kMfmaPer + 1, kMfmaPer - 1>(f, va, p_cur);
                 if constexpr (c == 0) moved = row_max_update(sbuf[B ^ 1], rs, alpha, c_log2);
                 exp_part<c * kExpPer, c * kExpPer, kExpPer>(sbuf[B ^ 1], p_lo[B ^ 1], rs.m, c_log2, sum);
 #pragma unroll
-                for (int x = 0; x < kMfmaPer; ++x)
+                for (int x = 1; x < kMfmaPer; ++x)
                 {
+                    __builtin_amdgcn_sched_group_barrier(kSchedDsRead, (kKPer + kMfmaPer - 2) / (kMfmaPer - 1), 0);
                     __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
-                    __builtin_amdgcn_sched_group_barrier(kSchedValu, 12, 0);
+                    __builtin_amdgcn_sched_group_barrier(kSchedValu, 10, 0);
                 }
                 __builtin_amdgcn_sched_barrier(0);
             });

@@ -25,8 +25,8 @@ constexpr int kFusedStages = 4;   // LDS stages per tensor (K, V) per wave group
 //            barrier;
 //   block B  read the K operands of tile jj + 2; DMA V tile jj + kFusedVAhead;
 //   end      wait for the LDS reads; barrier.
-// The prologue copies K_0 .. K_3 and V_0 .. V_2 and reads the K operands of
-// tiles 0 and 1 itself.
+// The prologue copies K_0 .. K_3 and V_0 .. V_2, waits for K_0 and reads
+// its operands, then waits for every prologue copy and reads K_1's operands.
 constexpr int kFusedKAhead = kFusedStages;      // into K_jj's stage (read in step jj - 2)
 constexpr int kFusedVAhead = kFusedStages - 1;  // into V_{jj-1}'s stage (read in step jj - 1)
 

@@ -11,8 +11,10 @@ per-step actions and checks, for every tile count:
       step argument equals jj % kFusedUnroll;
   (b) both groups reach the same total, split.barriers, after padding;
   (c) every K / V stage is read only after the DMA that filled it was waited
-      for and a barrier passed, and no DMA targets a stage whose tile is still
-      to be read (so every read sees the tile it expects).
+      for (the model's waits are the kernel's vmcnt waits: all copy groups but
+      the last n issued have landed) and a barrier passed, and no DMA targets
+      a stage whose tile is still to be read (so every read sees the tile it
+      expects).
 """
 import os
 import subprocess
@@ -27,14 +29,13 @@ PROGRAM = r'''
 using namespace fa;
 constexpr int S = kFusedStages;
 
-// A stage's state: which tile it holds, when its copy was issued (epoch =
-// barriers passed at issue time, plus the step-local order) and whether the
-// wave has waited for it.
-struct Stage { int tile = -1; int issue_seq = -1; bool landed = false; int landed_epoch = -1; };
+// A stage's state: which tile it holds, the copy group that filled it (issue
+// order), and whether and when (barrier epoch) the wave has waited for it.
+struct Stage { int tile = -1; int group = -1; bool landed = false; int landed_epoch = -1; };
 
 long bad = 0;
 int epoch = 0;      // workgroup barriers passed
-int seq = 0;        // copy issue sequence number
+int groups = 0;     // copy groups issued (one group = one tile's kIssues copies)
 std::vector<Stage> ks, vs;
 
 // Copy `tile` into stage `st`; the stage's previous tile must have been
@@ -42,13 +43,14 @@ std::vector<Stage> ks, vs;
 // barrier (`consumed` = highest tile of that tensor whose reads are done).
 void dma(std::vector<Stage>& arr, int st, int tile, int consumed) {
     if (arr[st].tile >= 0 && arr[st].tile > consumed) ++bad;
-    arr[st] = Stage{tile, seq++, false, -1};
+    arr[st] = Stage{tile, groups++, false, -1};
 }
-// vmcnt-style wait: every copy issued before `keep_from_seq` has landed.
-void wait_before(int keep_from_seq) {
+// s_waitcnt vmcnt(n * kIssues): every copy group except the last n issued
+// has landed (copies complete in issue order).
+void wait_allow(int n) {
     for (auto* a : {&ks, &vs})
         for (auto& s : *a)
-            if (!s.landed && s.issue_seq >= 0 && s.issue_seq < keep_from_seq) { s.landed = true; s.landed_epoch = epoch; }
+            if (!s.landed && s.group >= 0 && s.group < groups - n) { s.landed = true; s.landed_epoch = epoch; }
 }
 void barrier() { ++epoch; }
 // A read needs the expected tile, landed before the most recent barrier.
@@ -62,30 +64,28 @@ int main() {
         if (sp.count0 + sp.count1 != n_tiles || sp.count0 < sp.count1 || sp.first1 != sp.count0) ++bad;
         for (int g = 0; g < 2; ++g) {
             const int cnt = g == 0 ? sp.count0 : sp.count1;
-            ks.assign(S, Stage{}); vs.assign(S, Stage{}); epoch = 0; seq = 0;
-            // prologue: K_0..K_{S-1}, V_0..V_{S-2}; wait for K_0; barrier
+            ks.assign(S, Stage{}); vs.assign(S, Stage{}); epoch = 0; groups = 0;
+            // prologue: K_0 .. K_{S-1}, V_0 .. V_{S-2}
             for (int x = 0; x < S; ++x) dma(ks, x, x, -1);
-            const int after_k0 = 1;  // copies issued after K_0 may fly
             for (int x = 0; x < S - 1; ++x) dma(vs, x, x, -1);
-            wait_before(after_k0);
+            wait_allow(2 * S - 2);                       // Q and K_0 landed
             barrier();
             int barriers = 1;
             if (cnt > 0) read(ks, 0, 0);                 // S^T of tile 0
-            wait_before(seq); barrier(); ++barriers;     // all prologue copies landed
+            wait_allow(0);                               // every prologue copy landed
+            barrier(); ++barriers;
             if (cnt > 1) read(ks, 1 % S, 1);             // K operands of tile 1
             if (g == 1) { barrier(); ++barriers; }       // half-step offset
             int k_consumed = 1, v_consumed = -1;
-            int prev_first_seq = seq;                    // first copy of step jj-1
             int steps = 0;
             fused_group_walk(cnt, [&](auto par, int jj) {
                 ++steps;
                 if (decltype(par)::value != jj % kFusedUnroll) ++bad;
                 // block A: V operands of tile jj; copies of K tile jj+KAhead
                 read(vs, jj % S, jj);
-                const int step_first_seq = seq;
                 dma(ks, (jj + kFusedKAhead) % S, jj + kFusedKAhead, k_consumed);
-                // mid: only copies of steps jj-1 and jj may fly
-                wait_before(prev_first_seq);
+                // mid: the last three copy groups may still fly
+                wait_allow(3);
                 barrier(); ++barriers;
                 // block B: K operands of tile jj+2; copies of V tile jj+VAhead
                 if (jj + 2 < cnt) read(ks, (jj + 2) % S, jj + 2);
@@ -93,7 +93,6 @@ int main() {
                 barrier(); ++barriers;                   // end: LDS reads done
                 v_consumed = jj;
                 k_consumed = jj + 2;
-                prev_first_seq = step_first_seq;
             });
             if (steps != cnt) ++bad;
             if (barriers != fused_group_barriers(g, cnt)) ++bad;
@@ -119,13 +118,14 @@ def test_schedule_barriers_and_stages(tmp_path):
 
 def test_schedule_checker_catches_a_short_pipeline(tmp_path):
     """Planted mistakes: a K prefetch two tiles further ahead overwrites a
-    stage still to be read, and a mid-step wait that lets one more step of
-    copies fly reads a stage before its copy landed; the checker must report
-    both."""
+    stage still to be read; a mid-step wait that lets one more copy group fly,
+    and a prologue wait that lets the last prologue copies fly, read a stage
+    before its copy landed. The checker must report each."""
     plants = [
         ("dma(ks, (jj + kFusedKAhead) % S, jj + kFusedKAhead, k_consumed);",
          "dma(ks, (jj + kFusedKAhead + 2) % S, jj + kFusedKAhead + 2, k_consumed);"),
-        ("prev_first_seq = step_first_seq;", "prev_first_seq = jj > 0 ? prev_first_seq : step_first_seq;"),
+        ("wait_allow(3);", "wait_allow(4);"),
+        ("wait_allow(0);                               // every", "wait_allow(3);                               // every"),
     ]
     for i, (old, new) in enumerate(plants):
         assert old in PROGRAM
