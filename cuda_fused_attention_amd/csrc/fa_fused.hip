@@ -55,11 +55,16 @@
 //     max grows by more than 2^8, then O and the row sum are rescaled; P stays
 //     <= 256. Row sums accumulate the bf16-rounded P with v_dot2_f32_bf16, the
 //     same weights the PV MFMA uses.
-//   * Causal: a wave skips tiles wholly above its diagonal, only tiles that
-//     cross the diagonal or the sequence end pay for the per-element mask
-//     (-inf), and workgroups are issued heaviest-first. Workgroup ids are
-//     remapped so that all query blocks of a (batch, head) slab run on one XCD
-//     and share its L2 (measured: K and V are read from HBM once).
+//   * Causal: a wave skips tiles wholly above its diagonal, and only tiles
+//     that cross the diagonal or the sequence end pay for the per-element
+//     mask (-inf). A workgroup owns two half blocks of rows, an early one and
+//     its mirror from the end of the sequence, so all workgroups carry about
+//     the same number of (row, key) pairs instead of the last one carrying a
+//     full dense row of tiles; within each SIMD one wave holds early rows and
+//     one late rows.
+//   * Workgroup ids are remapped so that all query blocks of a (batch, head)
+//     slab run on one XCD and share its L2 (measured: K and V are read from
+//     HBM once).
 
 #include <cmath>
 #include <cstdint>
@@ -428,9 +433,37 @@ __global__ __launch_bounds__(128 * kWpg) void fused_attention_kernel(const uint1
     const int logical = fa::xcd_remap(static_cast<int>(blockIdx.x), total_blocks);
     const int slab = logical / q_blocks;
     const int qb_in = logical % q_blocks;
-    const int qb = kCausal ? (q_blocks - 1 - qb_in) : qb_in;  // causal: heaviest first
-    const int q0 = qb * C::kRows;
-    const int wq0 = q0 + 32 * wg_s;  // uniform: the tile bounds below stay scalar
+
+    // Row slot of this wave: the 32 query rows it owns. Wave w of group 0
+    // and the group-1 wave with the same slot hold the two KV halves of the
+    // same rows and are merged at the end. Values are uniform (SGPRs), so
+    // the tile bounds derived from them stay scalar.
+    //   Dense: the workgroup owns kRows consecutive rows, slot s = wave w.
+    //   Causal: the workgroup owns two half blocks of kRows/2 rows, an
+    //   early one (pair index p) and its mirror (last - p), so every
+    //   workgroup carries about the same work (a triangle's rows p and
+    //   last - p sum to a constant); slots [0, kWpg/2) are the early half
+    //   block. Group 0's waves take slots 0..kWpg-1 in order and group 1's
+    //   are rotated by kWpg/2, so the two waves sharing a SIMD (w and
+    //   w + kWpg) hold one early and one late half block.
+    const int grp_s = __builtin_amdgcn_readfirstlane(grp);
+    const int slot = (kCausal && grp_s == 1) ? (wg_s + kWpg / 2) % kWpg : wg_s;
+    constexpr int kHalfRows = C::kRows / 2;
+    int wq0, last_row;
+    if constexpr (kCausal)
+    {
+        const int n_half = (n + kHalfRows - 1) / kHalfRows;
+        const int pa = qb_in;
+        const int pb = n_half - 1 - qb_in;  // == pa for the middle of an odd count: no partner
+        const int half = slot < kWpg / 2 ? pa : (pb > pa ? pb : n_half);  // n_half: rows past n, idle
+        wq0 = half * kHalfRows + 32 * (slot % (kWpg / 2));
+        last_row = (pb > pa ? pb : pa) * kHalfRows + kHalfRows - 1;
+    }
+    else
+    {
+        wq0 = qb_in * C::kRows + 32 * slot;
+        last_row = qb_in * C::kRows + C::kRows - 1;
+    }
 
     const size_t slab_off = static_cast<size_t>(slab) * n * D;
     const uint16_t* q_slab = q + slab_off;
@@ -438,7 +471,7 @@ __global__ __launch_bounds__(128 * kWpg) void fused_attention_kernel(const uint1
     const ScalarPtr k_bytes = scalar_ptr(k + slab_off);
     const ScalarPtr v_bytes = scalar_ptr(v + slab_off);
 
-    const int last_key = kCausal ? min(q0 + C::kRows - 1, n - 1) : n - 1;
+    const int last_key = kCausal ? min(last_row, n - 1) : n - 1;
     const int n_tiles = last_key / kTileKV + 1;
     const fa::FusedSplit split = fa::fused_split(n_tiles);
 
@@ -450,7 +483,9 @@ __global__ __launch_bounds__(128 * kWpg) void fused_attention_kernel(const uint1
     // Dense: t_last is n_tiles - 1, passed through readfirstlane so the
     // compiler cannot fold the per-step tests away; folded, it merges the
     // step variants and its hoisting then spills at head_dim 128.
-    const int t_last = kCausal ? min((wq0 + 31) / kTileKV, n_tiles - 1) : __builtin_amdgcn_readfirstlane(n_tiles - 1);
+    // Causal waves whose rows all lie past the sequence end compute nothing.
+    const int t_last = kCausal ? (wq0 >= n ? -1 : min((wq0 + 31) / kTileKV, n_tiles - 1))
+                               : __builtin_amdgcn_readfirstlane(n_tiles - 1);
 
     const int query = wq0 + i;
     // First key this lane's query may not see, minus 4*h (see mask_tile).
@@ -693,8 +728,8 @@ __global__ __launch_bounds__(128 * kWpg) void fused_attention_kernel(const uint1
     // Merge: group 1 stages its (exponent base, partial sums, O^T) in LDS,
     // group 0 folds them into its own and writes O. All DMAs have landed
     // (every wave drained its own before the last barrier).
-    float* const ostage = reinterpret_cast<float*>(lds) + wg * C::kOStageFloats;
-    float* const ml_stage = reinterpret_cast<float*>(lds) + kWpg * C::kOStageFloats + wg * 128;
+    float* const ostage = reinterpret_cast<float*>(lds) + slot * C::kOStageFloats;
+    float* const ml_stage = reinterpret_cast<float*>(lds) + kWpg * C::kOStageFloats + slot * 128;
     if (grp == 1)
     {
 #pragma unroll
@@ -791,8 +826,11 @@ int launch_fused(const void* q, const void* k, const void* v, void* o, int batch
     if (mis & 15u) return hipErrorInvalidValue;
     // DMA offsets are 32-bit byte offsets within one (batch, head) slab.
     if (static_cast<long long>(seq_len) * head_dim * 2 > 0x7fffffffLL) return hipErrorInvalidValue;
+    // Workgroups per slab: dense, one per 32*kWpg rows; causal, one per
+    // pair of 16*kWpg-row half blocks (p, last - p).
     constexpr int rows = 32 * kWpg;
-    const long long q_blocks = (static_cast<long long>(seq_len) + rows - 1) / rows;
+    const long long q_blocks = causal ? ((static_cast<long long>(seq_len) + rows / 2 - 1) / (rows / 2) + 1) / 2
+                                      : (static_cast<long long>(seq_len) + rows - 1) / rows;
     const long long total = bh * q_blocks;
     if (total > 0x7fffffffLL / (128 * kWpg)) return hipErrorInvalidValue;
 
