@@ -66,6 +66,7 @@
 //     slab run on one XCD and share its L2 (measured: K and V are read from
 //     HBM once).
 
+#include <atomic>
 #include <cmath>
 #include <cstdint>
 #include <type_traits>
@@ -414,7 +415,7 @@ __global__ __launch_bounds__(128 * kWpg) void fused_attention_kernel(const uint1
                                                                      const uint16_t* __restrict__ v,
                                                                      uint16_t* __restrict__ o, int n,
                                                                      int q_blocks, int total_blocks,
-                                                                     float c_log2)
+                                                                     float c_log2, int paired)
 {
     using C = Cfg<D, kWpg>;
     // Group g's K stages, then its V stages, at compile-time offsets of one
@@ -438,19 +439,23 @@ __global__ __launch_bounds__(128 * kWpg) void fused_attention_kernel(const uint1
     // and the group-1 wave with the same slot hold the two KV halves of the
     // same rows and are merged at the end. Values are uniform (SGPRs), so
     // the tile bounds derived from them stay scalar.
-    //   Dense: the workgroup owns kRows consecutive rows, slot s = wave w.
-    //   Causal: the workgroup owns two half blocks of kRows/2 rows, an
-    //   early one (pair index p) and its mirror (last - p), so every
-    //   workgroup carries about the same work (a triangle's rows p and
-    //   last - p sum to a constant); slots [0, kWpg/2) are the early half
-    //   block. Group 0's waves take slots 0..kWpg-1 in order and group 1's
-    //   are rotated by kWpg/2, so the two waves sharing a SIMD (w and
-    //   w + kWpg) hold one early and one late half block.
+    //   Dense, and causal grids of several workgroup rounds: the workgroup
+    //   owns kRows consecutive rows, slot s = wave w; causal blocks are
+    //   issued heaviest first, so the dispatcher balances the rounds.
+    //   Causal grids of one round (`paired`): the workgroup owns two half
+    //   blocks of kRows/2 rows, an early one (pair index p) and its mirror
+    //   (last - p), so every workgroup carries about the same work (a
+    //   triangle's rows p and last - p sum to a constant); slots
+    //   [0, kWpg/2) are the early half block. Group 0's waves take slots
+    //   0..kWpg-1 in order and group 1's are rotated by kWpg/2, so the two
+    //   waves sharing a SIMD (w and w + kWpg) hold one early and one late
+    //   half block.
     const int grp_s = __builtin_amdgcn_readfirstlane(grp);
-    const int slot = (kCausal && grp_s == 1) ? (wg_s + kWpg / 2) % kWpg : wg_s;
+    const bool pair_rows = kCausal && paired != 0;
+    const int slot = (pair_rows && grp_s == 1) ? (wg_s + kWpg / 2) % kWpg : wg_s;
     constexpr int kHalfRows = C::kRows / 2;
     int wq0, last_row;
-    if constexpr (kCausal)
+    if (pair_rows)
     {
         const int n_half = (n + kHalfRows - 1) / kHalfRows;
         const int pa = qb_in;
@@ -461,8 +466,9 @@ __global__ __launch_bounds__(128 * kWpg) void fused_attention_kernel(const uint1
     }
     else
     {
-        wq0 = qb_in * C::kRows + 32 * slot;
-        last_row = qb_in * C::kRows + C::kRows - 1;
+        const int qb = kCausal ? (q_blocks - 1 - qb_in) : qb_in;
+        wq0 = qb * C::kRows + 32 * slot;
+        last_row = qb * C::kRows + C::kRows - 1;
     }
 
     const size_t slab_off = static_cast<size_t>(slab) * n * D;
@@ -805,10 +811,27 @@ const void* pick_kernel(int head_dim, bool causal)
 
 template <int D, int kWpg, bool kCausal>
 void launch_typed(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o, int n, int q_blocks,
-                  int total, float c_log2, hipStream_t stream)
+                  int total, float c_log2, int paired, hipStream_t stream)
 {
     hipLaunchKernelGGL((fused_attention_kernel<D, kWpg, kCausal>), dim3(static_cast<unsigned>(total)),
-                       dim3(Cfg<D, kWpg>::kThreads), 0, stream, q, k, v, o, n, q_blocks, total, c_log2);
+                       dim3(Cfg<D, kWpg>::kThreads), 0, stream, q, k, v, o, n, q_blocks, total, c_log2, paired);
+}
+
+// Compute units of the current device (cached per device; 256 on an
+// MI355X). A failed query only affects the causal work layout choice.
+int device_compute_units()
+{
+    constexpr int kMaxDevices = 64;
+    static std::atomic<int> cache[kMaxDevices];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 256;
+    int cus = cache[dev].load(std::memory_order_relaxed);
+    if (cus <= 0)
+    {
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+        cache[dev].store(cus, std::memory_order_relaxed);
+    }
+    return cus;
 }
 
 template <int kWpg>
@@ -826,11 +849,15 @@ int launch_fused(const void* q, const void* k, const void* v, void* o, int batch
     if (mis & 15u) return hipErrorInvalidValue;
     // DMA offsets are 32-bit byte offsets within one (batch, head) slab.
     if (static_cast<long long>(seq_len) * head_dim * 2 > 0x7fffffffLL) return hipErrorInvalidValue;
-    // Workgroups per slab: dense, one per 32*kWpg rows; causal, one per
-    // pair of 16*kWpg-row half blocks (p, last - p).
+    // Workgroups per slab: one per 32*kWpg rows; causal grids that fit in
+    // one round on the device instead get one per pair of 16*kWpg-row half
+    // blocks (p, last - p), which evens out the triangle's work per
+    // workgroup. Larger causal grids keep whole blocks, issued heaviest
+    // first, and the dispatcher balances the rounds.
     constexpr int rows = 32 * kWpg;
-    const long long q_blocks = causal ? ((static_cast<long long>(seq_len) + rows / 2 - 1) / (rows / 2) + 1) / 2
-                                      : (static_cast<long long>(seq_len) + rows - 1) / rows;
+    const long long blocks = (static_cast<long long>(seq_len) + rows - 1) / rows;
+    const int paired = (causal && bh * blocks <= device_compute_units()) ? 1 : 0;
+    const long long q_blocks = paired ? ((static_cast<long long>(seq_len) + rows / 2 - 1) / (rows / 2) + 1) / 2 : blocks;
     const long long total = bh * q_blocks;
     if (total > 0x7fffffffLL / (128 * kWpg)) return hipErrorInvalidValue;
 
@@ -844,13 +871,13 @@ int launch_fused(const void* q, const void* k, const void* v, void* o, int batch
     const int tot = static_cast<int>(total);
     if (head_dim == 64)
     {
-        if (causal) launch_typed<64, kWpg, true>(qb, kb, vb, ob, seq_len, qbk, tot, c_log2, stream);
-        else launch_typed<64, kWpg, false>(qb, kb, vb, ob, seq_len, qbk, tot, c_log2, stream);
+        if (causal) launch_typed<64, kWpg, true>(qb, kb, vb, ob, seq_len, qbk, tot, c_log2, paired, stream);
+        else launch_typed<64, kWpg, false>(qb, kb, vb, ob, seq_len, qbk, tot, c_log2, 0, stream);
     }
     else
     {
-        if (causal) launch_typed<128, kWpg, true>(qb, kb, vb, ob, seq_len, qbk, tot, c_log2, stream);
-        else launch_typed<128, kWpg, false>(qb, kb, vb, ob, seq_len, qbk, tot, c_log2, stream);
+        if (causal) launch_typed<128, kWpg, true>(qb, kb, vb, ob, seq_len, qbk, tot, c_log2, paired, stream);
+        else launch_typed<128, kWpg, false>(qb, kb, vb, ob, seq_len, qbk, tot, c_log2, 0, stream);
     }
     return static_cast<int>(hipGetLastError());
 }

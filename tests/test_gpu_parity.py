@@ -102,6 +102,25 @@ def test_multi_slab_ragged(fa, oracle_mod):
                 check(oracle_mod, run_bits(fa, kernel, q, k, v, causal), ref, f"ragged {kernel} {(B, H, N, D, causal)}")
 
 
+def test_causal_work_layouts(fa, oracle_mod):
+    """Causal grids that fit one round on the device pair an early and a late
+    half block per workgroup; larger grids keep whole blocks issued heaviest
+    first. Both layouts, with even and odd half-block counts (an odd count
+    leaves the middle half block without a partner), against the oracle."""
+    cases = [
+        (1, 300, 192, 64),   # 300 slabs: more workgroups than CUs -> whole blocks
+        (2, 4, 1000, 128),   # one round -> pairs; 16 half blocks of 64 rows (v3)
+        (1, 3, 1100, 64),    # one round -> pairs; 18 half blocks (v3), 35 (v3b): odd
+        (1, 1, 2049, 128),   # one slab, tail row in its own half block
+    ]
+    for (B, H, N, D) in cases:
+        q, k, v = oracle_mod.make_inputs(B, H, N, D, seeds={"q": 41, "k": 42, "v": 43})
+        ref = oracle_mod.attention(q, k, v, True, threads=HOST_THREADS)
+        for kernel in ("v3_mfma", "v3b_mfma"):
+            say("causal layout", kernel, B, H, N, D)
+            check(oracle_mod, run_bits(fa, kernel, q, k, v, True), ref, f"causal layout {kernel} {(B, H, N, D)}")
+
+
 def test_v3_and_v3b_agree(fa, oracle_mod):
     """Dense: each wave computes its 32 rows identically whatever the workgroup
     size (both configurations split the same KV range the same way), so the
