@@ -79,6 +79,7 @@ namespace {
 
 using fa::bf16x8;
 using fa::f32x16;
+using fa::f32x4;
 
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void;
@@ -99,11 +100,9 @@ struct Cfg
     static constexpr int kIssues = kTileKV / (kRowsPerIssue * kWpg);   // DMA issues per wave per tile
     static constexpr int kGroupElems = 2 * kStages * kTileElems;       // one group's K and V stages
     static constexpr int kLdsElems = 2 * kGroupElems;
-    static constexpr int kOStageFloats = (D / 32) * 16 * 64;           // one wave's O^T
     static_assert(D == 64 || D == 128, "head_dim 64 or 128");
     static_assert(kIssues * kRowsPerIssue * kWpg == kTileKV, "tile splits evenly over a group");
     static_assert(2 * kIssues < 64, "vmcnt range");
-    static_assert(kWpg * (kOStageFloats + 128) * 4 <= kLdsElems * 2, "merge staging fits the LDS array");
 };
 
 // s_waitcnt with vmcnt <= N and lgkmcnt == 0 (expcnt untouched).
@@ -731,68 +730,90 @@ __global__ __launch_bounds__(128 * kWpg) void fused_attention_kernel(const uint1
     if (grp == 0) run_group(std::integral_constant<int, 0>{});
     else run_group(std::integral_constant<int, 1>{});
 
-    // Merge: group 1 stages its (exponent base, partial sums, O^T) in LDS,
-    // group 0 folds them into its own and writes O. All DMAs have landed
-    // (every wave drained its own before the last barrier).
-    float* const ostage = reinterpret_cast<float*>(lds) + slot * C::kOStageFloats;
-    float* const ml_stage = reinterpret_cast<float*>(lds) + kWpg * C::kOStageFloats + slot * 128;
-    if (grp == 1)
-    {
+    // Merge and epilogue, split over both groups: the wave of group g
+    // finalises head dims [g*D/2, (g+1)*D/2) of its slot's 32 rows. It sends
+    // the other half of its O^T, its exponent base and its partial row sums
+    // to the other group's wave with the same slot through LDS, folds the
+    // half it receives into its own, normalises, and stores its half of the
+    // rows. All DMAs have landed (every wave drained its own before the last
+    // barrier), so the stage area is free.
+    auto finish = [&](auto gtag) {
+        constexpr int G = decltype(gtag)::value;
+        constexpr int kHalfDb = D / 64;               // 32-dim blocks per half
+        constexpr int kXFloats = kHalfDb * 16 * 64;   // one wave's half of O^T
+        constexpr int kXSlot = 2 * (kXFloats + 128);  // both directions of one slot
+        static_assert(kWpg * kXSlot * 4 <= C::kLdsElems * 2, "merge staging fits the LDS array");
+        float* const xslot = reinterpret_cast<float*>(lds) + slot * kXSlot;
+        float* const x_send = xslot + G * (kXFloats + 128);
+        float* const x_recv = xslot + (1 - G) * (kXFloats + 128);
+        constexpr int kKeep = G * kHalfDb;        // first 32-dim block finalised here
+        constexpr int kSend = (1 - G) * kHalfDb;  // first block sent to the partner
+        // Four consecutive accumulator elements per 16-byte write.
 #pragma unroll
-        for (int db = 0; db < D / 32; ++db)
+        for (int b = 0; b < kHalfDb; ++b)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) ostage[(db * 16 + r) * 64 + lane] = f.o[db][r];
-        ml_stage[lane] = rs.m;
-        ml_stage[64 + lane] = rs.l;
-    }
-    wait_vm_lgkm0<0>();
-    barrier();
-    if (grp == 1) return;
+            for (int r4 = 0; r4 < 4; ++r4)
+            {
+                const f32x4 v4 = {f.o[kSend + b][4 * r4], f.o[kSend + b][4 * r4 + 1], f.o[kSend + b][4 * r4 + 2],
+                                  f.o[kSend + b][4 * r4 + 3]};
+                *reinterpret_cast<f32x4*>(x_send + ((b * 4 + r4) * 64 + lane) * 4) = v4;
+            }
+        x_send[kXFloats + lane] = rs.m;
+        x_send[kXFloats + 64 + lane] = rs.l;
+        wait_vm_lgkm0<0>();
+        barrier();
 
-    {
-        const float m1 = ml_stage[lane];
-        const float l1 = ml_stage[64 + lane];
+        const float m1 = x_recv[kXFloats + lane];
+        const float l1 = x_recv[kXFloats + 64 + lane];
         const float m = __builtin_elementwise_maximum(rs.m, m1);
         const float a0 = __builtin_amdgcn_exp2f(rs.m - m);
         const float a1 = __builtin_amdgcn_exp2f(m1 - m);
-        rs.l = rs.l * a0 + l1 * a1;
+        const float l = rs.l * a0 + l1 * a1;
 #pragma unroll
-        for (int db = 0; db < D / 32; ++db)
+        for (int b = 0; b < kHalfDb; ++b)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) f.o[db][r] = f.o[db][r] * a0 + ostage[(db * 16 + r) * 64 + lane] * a1;
-    }
+            for (int r4 = 0; r4 < 4; ++r4)
+            {
+                const f32x4 x = *reinterpret_cast<const f32x4*>(x_recv + ((b * 4 + r4) * 64 + lane) * 4);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) f.o[kKeep + b][4 * r4 + j] = f.o[kKeep + b][4 * r4 + j] * a0 + x[j] * a1;
+            }
 
-    // Epilogue: the two lane halves hold partial row sums of the same query.
-    // O^T (lane = query) is transposed through this wave's own staging area
-    // (nothing else reads it any more) into row-major bf16 with XOR-swizzled
-    // 16-byte chunks, then stored as contiguous 16-byte pieces: the wave's
-    // 32 rows are one contiguous block of O.
-    const float l_tot = rs.l + __shfl_xor(rs.l, 32, 64);
-    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-    constexpr int kRowChunks = D / 8;
-    uint16_t* const obuf = reinterpret_cast<uint16_t*>(ostage);
+        // The two lane halves hold partial row sums of the same query. O^T
+        // (lane = query) is transposed through the received area (only this
+        // wave touches it now) into row-major bf16 with XOR-swizzled 16-byte
+        // chunks, then stored as contiguous 16-byte pieces of the rows.
+        const float l_tot = l + __shfl_xor(l, 32, 64);
+        const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+        constexpr int kHalfCols = D / 2;
+        constexpr int kHalfChunks = kHalfCols / 8;
+        uint16_t* const obuf = reinterpret_cast<uint16_t*>(x_recv);
+        wait_vm_lgkm0<0>();  // received values are in registers before the area is reused
 #pragma unroll
-    for (int db = 0; db < D / 32; ++db)
+        for (int b = 0; b < kHalfDb; ++b)
 #pragma unroll
-        for (int g = 0; g < 4; ++g)
+            for (int g = 0; g < 4; ++g)
+            {
+                uint2 packed;
+                packed.x = fa::pack_bf16x2(f.o[kKeep + b][4 * g + 0] * inv, f.o[kKeep + b][4 * g + 1] * inv);
+                packed.y = fa::pack_bf16x2(f.o[kKeep + b][4 * g + 2] * inv, f.o[kKeep + b][4 * g + 3] * inv);
+                const int chunk = (4 * b + g) ^ (i & (kHalfChunks - 1));
+                *reinterpret_cast<uint2*>(obuf + i * kHalfCols + chunk * 8 + 4 * h) = packed;
+            }
+        wait_vm_lgkm0<63>();
+#pragma unroll
+        for (int u = 0; u < kHalfChunks / 2; ++u)
         {
-            uint2 packed;
-            packed.x = fa::pack_bf16x2(f.o[db][4 * g + 0] * inv, f.o[db][4 * g + 1] * inv);
-            packed.y = fa::pack_bf16x2(f.o[db][4 * g + 2] * inv, f.o[db][4 * g + 3] * inv);
-            const int chunk = (4 * db + g) ^ (i & (kRowChunks - 1));
-            *reinterpret_cast<uint2*>(obuf + i * D + chunk * 8 + 4 * h) = packed;
+            const int x = u * 64 + lane;
+            const int row = x / kHalfChunks;
+            const int c = x % kHalfChunks;
+            const uint4 chunk = *reinterpret_cast<const uint4*>(obuf + row * kHalfCols + ((c ^ (row & (kHalfChunks - 1))) * 8));
+            if (wq0 + row < n)
+                *reinterpret_cast<uint4*>(o + slab_off + static_cast<size_t>(wq0 + row) * D + G * kHalfCols + c * 8) = chunk;
         }
-    wait_vm_lgkm0<63>();
-#pragma unroll
-    for (int u = 0; u < D / 16; ++u)
-    {
-        const int x = u * 64 + lane;
-        const int row = x / kRowChunks;
-        const int c = x % kRowChunks;
-        const uint4 chunk = *reinterpret_cast<const uint4*>(obuf + row * D + ((c ^ (row & (kRowChunks - 1))) * 8));
-        if (wq0 + row < n)
-            *reinterpret_cast<uint4*>(o + slab_off + static_cast<size_t>(wq0 + row) * D + c * 8) = chunk;
-    }
+    };
+    if (grp_s == 0) finish(std::integral_constant<int, 0>{});
+    else finish(std::integral_constant<int, 1>{});
 }
 
 template <int D, int kWpg, bool kCausal>
