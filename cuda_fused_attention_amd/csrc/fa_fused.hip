@@ -100,9 +100,14 @@ struct Cfg
     static constexpr int kIssues = kTileKV / (kRowsPerIssue * kWpg);   // DMA issues per wave per tile
     static constexpr int kGroupElems = 2 * kStages * kTileElems;       // one group's K and V stages
     static constexpr int kLdsElems = 2 * kGroupElems;
+    static constexpr int kQElems = kWpg * 32 * D;                      // Q rows of the kWpg slots
+    static constexpr int kQIssues = 32 * D * 2 / 1024;                 // DMA issues per slot's Q rows
+    static constexpr int kQIssuesPerWave = kWpg * kQIssues / (2 * kWpg);
     static_assert(D == 64 || D == 128, "head_dim 64 or 128");
     static_assert(kIssues * kRowsPerIssue * kWpg == kTileKV, "tile splits evenly over a group");
     static_assert(2 * kIssues < 64, "vmcnt range");
+    static_assert(kQIssuesPerWave * 2 * kWpg == kWpg * kQIssues, "Q copies split evenly over the waves");
+    static_assert((kLdsElems + kQElems) * 2 <= 160 * 1024, "LDS of one workgroup");
 };
 
 // s_waitcnt with vmcnt <= N and lgkmcnt == 0 (expcnt untouched).
@@ -418,8 +423,9 @@ __global__ __launch_bounds__(128 * kWpg) void fused_attention_kernel(const uint1
 {
     using C = Cfg<D, kWpg>;
     // Group g's K stages, then its V stages, at compile-time offsets of one
-    // LDS array, so every operand read is a per-lane base plus an immediate.
-    __shared__ __attribute__((aligned(16))) uint16_t lds[C::kLdsElems];
+    // LDS array, so every operand read is a per-lane base plus an immediate;
+    // the Q rows of the workgroup's slots follow.
+    __shared__ __attribute__((aligned(16))) uint16_t lds[C::kLdsElems + C::kQElems];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -453,26 +459,25 @@ __global__ __launch_bounds__(128 * kWpg) void fused_attention_kernel(const uint1
     const bool pair_rows = kCausal && paired != 0;
     const int slot = (pair_rows && grp_s == 1) ? (wg_s + kWpg / 2) % kWpg : wg_s;
     constexpr int kHalfRows = C::kRows / 2;
-    int wq0, last_row;
-    if (pair_rows)
-    {
-        const int n_half = (n + kHalfRows - 1) / kHalfRows;
-        const int pa = qb_in;
-        const int pb = n_half - 1 - qb_in;  // == pa for the middle of an odd count: no partner
-        const int half = slot < kWpg / 2 ? pa : (pb > pa ? pb : n_half);  // n_half: rows past n, idle
-        wq0 = half * kHalfRows + 32 * (slot % (kWpg / 2));
-        last_row = (pb > pa ? pb : pa) * kHalfRows + kHalfRows - 1;
-    }
-    else
-    {
-        const int qb = kCausal ? (q_blocks - 1 - qb_in) : qb_in;
-        wq0 = qb * C::kRows + 32 * slot;
-        last_row = qb * C::kRows + C::kRows - 1;
-    }
+    const int n_half = (n + kHalfRows - 1) / kHalfRows;
+    const int pa = qb_in;
+    const int pb = n_half - 1 - qb_in;  // == pa for the middle of an odd count: no partner
+    const int qb = kCausal ? (q_blocks - 1 - qb_in) : qb_in;
+    // First row of slot s (rows past n belong to no query: idle).
+    auto slot_row0 = [&](int s) {
+        if (pair_rows)
+        {
+            const int half = s < kWpg / 2 ? pa : (pb > pa ? pb : n_half);
+            return half * kHalfRows + 32 * (s % (kWpg / 2));
+        }
+        return qb * C::kRows + 32 * s;
+    };
+    const int wq0 = slot_row0(slot);
+    const int last_row = pair_rows ? (pb > pa ? pb : pa) * kHalfRows + kHalfRows - 1 : qb * C::kRows + C::kRows - 1;
 
     const size_t slab_off = static_cast<size_t>(slab) * n * D;
-    const uint16_t* q_slab = q + slab_off;
-    // K and V slab bases as uniform byte pointers (scalar registers).
+    // Q, K and V slab bases as uniform byte pointers (scalar registers).
+    const ScalarPtr q_bytes = scalar_ptr(q + slab_off);
     const ScalarPtr k_bytes = scalar_ptr(k + slab_off);
     const ScalarPtr v_bytes = scalar_ptr(v + slab_off);
 
@@ -527,13 +532,26 @@ __global__ __launch_bounds__(128 * kWpg) void fused_attention_kernel(const uint1
         // have landed. Step 0 waits for every prologue copy: the workgroups
         // of a slab then start their walks together and keep reading the
         // same tiles at about the same time, which the L2 serves best.
-#pragma unroll
-        for (int ks = 0; ks < D / 16; ++ks)
+        // Q: the workgroup's slots' rows go to the Q area by DMA, laid out
+        // like a K tile (32 rows, swizzled 16-byte chunks), each wave taking
+        // an equal share of the 1 KiB copies; rows past n read as zero.
         {
-            if (query < n)
-                f.q[ks] = *reinterpret_cast<const bf16x8*>(q_slab + static_cast<size_t>(query) * D + 16 * ks + 8 * h);
-            else
-                f.q[ks] = bf16x8{};
+            const int wave_s = __builtin_amdgcn_readfirstlane(wave);
+            const int sub_row = lane / C::kChunks;
+            const int pchunk = lane % C::kChunks;
+#pragma unroll
+            for (int t = 0; t < C::kQIssuesPerWave; ++t)
+            {
+                const int j = wave_s * C::kQIssuesPerWave + t;
+                const int qs = j / C::kQIssues;  // slot whose rows this copy moves
+                const int u = j % C::kQIssues;
+                const int row0 = slot_row0(qs);
+                const int row = u * C::kRowsPerIssue + sub_row;
+                const uint32_t voff = static_cast<uint32_t>(row * (D * 2) + ((pchunk ^ swz_k<D>(row)) * 16));
+                const uint32_t bytes = row0 < n ? static_cast<uint32_t>((n - row0) * (D * 2)) : 0u;
+                const i32x4 rsrc = make_rsrc(q_bytes, static_cast<uint32_t>(min(row0, n) * (D * 2)), bytes);
+                dma16(rsrc, voff, lds_addr(lds + C::kLdsElems + qs * 32 * D) + u * 1024);
+            }
         }
 #pragma unroll
         for (int x = 0; x < kStages; ++x)
@@ -572,6 +590,10 @@ __global__ __launch_bounds__(128 * kWpg) void fused_attention_kernel(const uint1
         // Q and K_0 resident (the later prologue copies may still fly).
         wait_vm_lgkm0<(2 * kStages - 2) * C::kIssues>();
         barrier();
+#pragma unroll
+        for (int ks = 0; ks < D / 16; ++ks)
+            f.q[ks] = *reinterpret_cast<const bf16x8*>(lds + C::kLdsElems + slot * 32 * D + i * D +
+                                                       (((2 * ks + h) ^ swz_k<D>(i)) << 3));
 
         // Pipeline registers: S^T and the first half of P of the current
         // tile, double-buffered by step parity (no register copies), the
