@@ -29,18 +29,17 @@
 //                read in the previous block B) while the VALU finishes tile
 //                jj's exponentials (second half); the wave issues its share
 //                of the DMA copies of K tile jj+4;
-//       mid:     wait until only the copies of steps jj-1 and jj are in
-//                flight, workgroup barrier;
+//       barrier: wait until only the copies of steps jj-1 and jj are in
+//                flight and every LDS read has completed, workgroup barrier
+//                (the step's only one);
 //       block B: the K operands of tile jj+2 are read; the MFMA pipe
 //                accumulates O^T += V^T P^T of tile jj while the VALU starts
 //                tile jj+1 (mask, row max, first half of the exponentials);
-//                the wave issues its share of the copies of V tile jj+3;
-//       end:     wait for the LDS reads, workgroup barrier.
+//                the wave issues its share of the copies of V tile jj+3.
 //     MFMA and VALU work of one wave are independent inside each block, so
 //     the instruction stream interleaves them (sched_group_barrier), with one
-//     DMA issue between consecutive MFMA chunks; the wave of the other group
-//     on the same SIMD runs half a step behind and fills the remaining gaps
-//     (s_setprio gives the block-B wave issue priority).
+//     DMA issue between consecutive MFMA chunks; the other group's wave on
+//     the same SIMD fills the remaining gaps.
 //   * K and V tiles go HBM -> LDS directly with buffer_load_dwordx4 ... lds
 //     (lane l of an issue lands at M0 + 16*l), four stages per tensor per
 //     group. The LDS rows are row-major with the 16-byte chunk index
@@ -618,12 +617,10 @@ __global__ __launch_bounds__(128 * kWpg) void fused_attention_kernel(const uint1
         wait_vm_lgkm0<0>();
         barrier();  // every prologue tile resident; K_0's stage is free
         load_k_ops<D>(lds + 1 * C::kTileElems, f, ka);  // K operands of tile 1 (used only if lw >= 1)
-        if (G == 1) barrier();  // group 1 runs half a step behind group 0
 
-        // Each step is two blocks separated by a workgroup barrier; with
-        // group 1 half a step behind, every SIMD always has one wave in
-        // block A and one in block B, and both blocks start with their MFMA
-        // operands already in registers. A block runs in kIssues chunks
+        // Each step is two blocks separated by the step's one workgroup
+        // barrier; both blocks start with their MFMA operands already in
+        // registers. A block runs in kIssues chunks
         // (hard scheduling fences between chunks): the chunk's first MFMA,
         // one DMA copy, then the rest of its MFMAs beside its share of the
         // operand reads for the other block and of the VALU work, so the
@@ -646,7 +643,6 @@ __global__ __launch_bounds__(128 * kWpg) void fused_attention_kernel(const uint1
         auto block_a = [&](auto par_tag, int jj) {
             constexpr int P = decltype(par_tag)::value;
             constexpr int B = P & 1;  // S / P register buffer of tile jj
-            __builtin_amdgcn_s_setprio(0);
             sbuf[B ^ 1] = f32x16{};
             float sum = 0.0f;
             static_for<0, kChunk>([&](auto ctag) {
@@ -674,9 +670,6 @@ __global__ __launch_bounds__(128 * kWpg) void fused_attention_kernel(const uint1
         auto block_b = [&](auto par_tag, int jj) {
             constexpr int P = decltype(par_tag)::value;
             constexpr int B = P & 1;
-            // The block-B wave (the longer block) wins issue arbitration
-            // against the block-A wave that shares its SIMD.
-            __builtin_amdgcn_s_setprio(1);
             // Diagonal / tail tile (uniform, rare): mask before the row max.
             // On the wave's last tile (jj == lw) the "next" S^T is a dummy
             // product with a landed stage: masking all of it makes the head a
@@ -723,12 +716,12 @@ __global__ __launch_bounds__(128 * kWpg) void fused_attention_kernel(const uint1
             block_a(par_tag, jj);
             // Only the copies of steps jj-1 and jj may still be in flight:
             // K_{jj+2} (read in block B) and V_{jj+1} (read in step jj+1)
-            // have landed and become visible.
+            // have landed and become visible after the barrier; every LDS
+            // read issued so far has completed, which frees the stages the
+            // next copies overwrite.
             wait_vm_lgkm0<3 * C::kIssues>();
             barrier();
             block_b(par_tag, jj);
-            wait_vm_lgkm0<63>();
-            barrier();
         });
         for (int jj = max(n_active, 0); jj < cnt; ++jj)
         {
@@ -739,8 +732,6 @@ __global__ __launch_bounds__(128 * kWpg) void fused_attention_kernel(const uint1
             barrier();
 #pragma unroll
             for (int u = 0; u < C::kIssues; ++u) copy_v(jj + fa::kFusedVAhead, (stage + fa::kFusedVAhead) % kStages, u);
-            wait_vm_lgkm0<63>();
-            barrier();
         }
         // Pad to the common barrier count of both groups.
         for (int b = fa::fused_group_barriers(G, cnt); b < split.barriers; ++b) barrier();

@@ -21,10 +21,12 @@ constexpr int kFusedStages = 4;   // LDS stages per tensor (K, V) per wave group
 // Pipeline of one group, local step jj (tile jj of the group):
 //   block A  read the V operands of tile jj (LDS -> registers); DMA K tile
 //            jj + kFusedKAhead (its copies spread between the MFMAs);
-//   mid      wait until only the DMAs of steps jj-1 and jj are in flight;
-//            barrier;
-//   block B  read the K operands of tile jj + 2; DMA V tile jj + kFusedVAhead;
-//   end      wait for the LDS reads; barrier.
+//   barrier  wait until only the DMAs of steps jj-1 and jj are in flight and
+//            every LDS read issued so far has completed; workgroup barrier;
+//   block B  read the K operands of tile jj + 2; DMA V tile jj + kFusedVAhead.
+// One barrier per step covers both hazards: K_{jj+2} and V_{jj+1} landed
+// before it (read after it), and every stage a later copy overwrites was
+// last read before it or before the previous step's barrier.
 // The prologue copies K_0 .. K_3 and V_0 .. V_2, waits for K_0 and reads
 // its operands, then waits for every prologue copy and reads K_1's operands.
 constexpr int kFusedKAhead = kFusedStages;      // into K_jj's stage (read in step jj - 2)
@@ -39,16 +41,16 @@ struct FusedSplit
 };
 
 // Barriers group `g` executes for `count` tiles: one after the prologue DMAs,
-// one after the prologue's first S tile, group 1's idle half step (it runs
-// half a step behind group 0), and two per step (mid and end). Both groups
-// then pad to FusedSplit::barriers and run the same fixed tail (drain, merge).
-FA_HD inline int fused_group_barriers(int g, int count) { return 2 + (g == 1 ? 1 : 0) + 2 * count; }
+// one after the prologue's first S tile, and one per step. Both groups run
+// in phase, pad to FusedSplit::barriers and run the same fixed tail (drain,
+// merge).
+FA_HD inline int fused_group_barriers(int /*g*/, int count) { return 2 + count; }
 
 // The step walk of one group over its `count` tiles: step(kk, jj) for
 // jj = 0 .. count-1 with kk = jj % kFusedUnroll as a compile-time
 // std::integral_constant: kk % kFusedStages is the LDS stage rotation and
-// kk % 2 the register double buffer of S and P. Each step runs exactly two
-// workgroup barriers.
+// kk % 2 the register double buffer of S and P. Each step runs exactly one
+// workgroup barrier.
 constexpr int kFusedUnroll = kFusedStages;
 static_assert(kFusedUnroll % 2 == 0, "the S / P double buffer needs an even unroll");
 

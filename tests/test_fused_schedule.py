@@ -9,7 +9,9 @@ test compiles it with g++, replays the walk with a model of the kernel's
 per-step actions and checks, for every tile count:
   (a) the walk performs fused_group_barriers() barriers and the compile-time
       step argument equals jj % kFusedUnroll;
-  (b) both groups reach the same total, split.barriers, after padding;
+  (b) both groups reach the same total, split.barriers, after padding (the
+      groups run in phase: every step of either group has one workgroup
+      barrier);
   (c) every K / V stage is read only after the DMA that filled it was waited
       for (the model's waits are the kernel's vmcnt waits: all copy groups but
       the last n issued have landed) and a barrier passed, and no DMA targets
@@ -75,8 +77,10 @@ int main() {
             wait_allow(0);                               // every prologue copy landed
             barrier(); ++barriers;
             if (cnt > 1) read(ks, 1 % S, 1);             // K operands of tile 1
-            if (g == 1) { barrier(); ++barriers; }       // half-step offset
-            int k_consumed = 1, v_consumed = -1;
+            // A stage is free once its reads are followed by a barrier:
+            // K_0 was read before the second prologue barrier; K_1 is read
+            // after it and freed by step 0's barrier.
+            int k_consumed = 0, k_pending = 1, v_consumed = -1;
             int steps = 0;
             fused_group_walk(cnt, [&](auto par, int jj) {
                 ++steps;
@@ -84,15 +88,16 @@ int main() {
                 // block A: V operands of tile jj; copies of K tile jj+KAhead
                 read(vs, jj % S, jj);
                 dma(ks, (jj + kFusedKAhead) % S, jj + kFusedKAhead, k_consumed);
-                // mid: the last three copy groups may still fly
+                // the step's one barrier: the last three copy groups may
+                // still fly; every LDS read issued so far has completed
                 wait_allow(3);
                 barrier(); ++barriers;
+                v_consumed = jj;
+                k_consumed = k_pending;
                 // block B: K operands of tile jj+2; copies of V tile jj+VAhead
                 if (jj + 2 < cnt) read(ks, (jj + 2) % S, jj + 2);
+                k_pending = jj + 2;
                 dma(vs, (jj + kFusedVAhead) % S, jj + kFusedVAhead, v_consumed);
-                barrier(); ++barriers;                   // end: LDS reads done
-                v_consumed = jj;
-                k_consumed = jj + 2;
             });
             if (steps != cnt) ++bad;
             if (barriers != fused_group_barriers(g, cnt)) ++bad;
