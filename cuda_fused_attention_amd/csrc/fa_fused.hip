@@ -37,9 +37,9 @@
 //                tile jj+1 (mask, row max, first half of the exponentials);
 //                the wave issues its share of the copies of V tile jj+3.
 //     MFMA and VALU work of one wave are independent inside each block, so
-//     the instruction stream interleaves them (sched_group_barrier), with one
-//     DMA issue between consecutive MFMA chunks; the other group's wave on
-//     the same SIMD fills the remaining gaps.
+//     the compiler interleaves them within each chunk (scheduling fences
+//     keep the chunks apart), with one DMA issue per chunk; the other
+//     group's wave on the same SIMD fills the remaining gaps.
 //   * K and V tiles go HBM -> LDS directly with buffer_load_dwordx4 ... lds
 //     (lane l of an issue lands at M0 + 16*l), four stages per tensor per
 //     group. The LDS rows are row-major with the 16-byte chunk index
@@ -243,11 +243,6 @@ struct Frag
     int k_off[D / 16];      // per-lane LDS byte offsets of the K A-operand reads
     int v_off[D / 32];      // per-lane LDS byte offsets of the V tr16 reads
 };
-
-// Scheduling-group masks for __builtin_amdgcn_sched_group_barrier.
-constexpr int kSchedValu = 0x002;
-constexpr int kSchedMfma = 0x008;
-constexpr int kSchedDsRead = 0x100;
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 
@@ -620,11 +615,11 @@ __global__ __launch_bounds__(128 * kWpg) void fused_attention_kernel(const uint1
 
         // Each step is two blocks separated by the step's one workgroup
         // barrier; both blocks start with their MFMA operands already in
-        // registers. A block runs in kIssues chunks
-        // (hard scheduling fences between chunks): the chunk's first MFMA,
-        // one DMA copy, then the rest of its MFMAs beside its share of the
-        // operand reads for the other block and of the VALU work, so the
-        // matrix pipe starts at the top of every chunk and the copies
+        // registers. A block runs in kIssues chunks (hard scheduling fences
+        // between chunks): the chunk's first MFMA, one DMA copy, then the
+        // rest of its MFMAs beside its share of the operand reads for the
+        // other block and of the VALU work, interleaved by the compiler, so
+        // the matrix pipe starts at the top of every chunk and the copies
         // trickle into the memory pipeline instead of stalling the wave in a
         // burst.
         //   Block A: V operand reads of tile jj; copies of K tile jj+4;
@@ -654,13 +649,6 @@ __global__ __launch_bounds__(128 * kWpg) void fused_attention_kernel(const uint1
                 load_v_ops<D, c * kVPer, kVPer>(lds + (P % kStages) * C::kTileElems, f, va);
                 qk_part<D, c * kMfmaPer + 1, kMfmaPer - 1>(f, ka, sbuf[B ^ 1]);
                 exp_part<8 + c * kExpPer, c * kExpPer, kExpPer>(sbuf[B], p_hi, rs.m, c_log2, sum);
-#pragma unroll
-                for (int x = 1; x < kMfmaPer; ++x)
-                {
-                    __builtin_amdgcn_sched_group_barrier(kSchedDsRead, (4 * kVPer + kMfmaPer - 2) / (kMfmaPer - 1), 0);
-                    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
-                    __builtin_amdgcn_sched_group_barrier(kSchedValu, 8, 0);
-                }
                 __builtin_amdgcn_sched_barrier(0);
             });
             rs.l += sum;
@@ -691,13 +679,6 @@ __global__ __launch_bounds__(128 * kWpg) void fused_attention_kernel(const uint1
                 pv_part<D, c * kMfmaPer + 1, kMfmaPer - 1>(f, va, p_cur);
                 if constexpr (c == 0) moved = row_max_update(sbuf[B ^ 1], rs, alpha, c_log2);
                 exp_part<c * kExpPer, c * kExpPer, kExpPer>(sbuf[B ^ 1], p_lo[B ^ 1], rs.m, c_log2, sum);
-#pragma unroll
-                for (int x = 1; x < kMfmaPer; ++x)
-                {
-                    __builtin_amdgcn_sched_group_barrier(kSchedDsRead, (kKPer + kMfmaPer - 2) / (kMfmaPer - 1), 0);
-                    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
-                    __builtin_amdgcn_sched_group_barrier(kSchedValu, 10, 0);
-                }
                 __builtin_amdgcn_sched_barrier(0);
             });
             rs.l += sum;
