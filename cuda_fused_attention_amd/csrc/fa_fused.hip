@@ -338,6 +338,7 @@ constexpr float kEmptyBase = -1.0e30f;
 struct RowState
 {
     float m = kEmptyBase;  // exponent base, log2 domain, wave-lazily raised
+    float thr;             // raw score above which the base must move: (m + kRescaleLog2) / c_log2
     float l = 0.0f;        // partial row sum of the bf16-rounded P
 };
 
@@ -369,33 +370,35 @@ __device__ __forceinline__ void mask_tile(f32x16& s, int limit)
         if (8 * (r >> 2) + (r & 3) >= limit) s[r] = -INFINITY;
 }
 
-// Row max of a tile and the lazy base update: the base only moves when some
-// row's max exceeds it by more than 2^8 (wave-uniform decision, returned);
-// then l is scaled here and O by the caller (by `alpha`) once the MFMAs that
-// still use the old base are issued.
-// Row max of a tile's scores in the log2 domain (scaled by c_log2). IEEE
-// maximum (v_maximum3_f32) needs no operand canonicalisation; the other half
-// of the row sits in lane l^32 (v_permlane32_swap).
-__device__ __forceinline__ float row_max_log2(const f32x16& s, float c_log2)
+// Raw (unscaled) row max of a tile's scores: a v_maximum3_f32 tree over
+// the lane's 16 values (IEEE maximum needs no operand canonicalisation),
+// then the other half of the row from lane l^32 (v_permlane32_swap).
+__device__ __forceinline__ float row_max_raw(const f32x16& s)
 {
-    float mx = __builtin_elementwise_maximum(s[0], s[1]);
-#pragma unroll
-    for (int r = 2; r < 16; r += 2) mx = __builtin_elementwise_maximum(mx, __builtin_elementwise_maximum(s[r], s[r + 1]));
+    auto max3 = [](float a, float b, float c) {
+        return __builtin_elementwise_maximum(__builtin_elementwise_maximum(a, b), c);
+    };
+    const float a0 = max3(s[0], s[1], s[2]);
+    const float a1 = max3(s[3], s[4], s[5]);
+    const float a2 = max3(s[6], s[7], s[8]);
+    const float a3 = max3(s[9], s[10], s[11]);
+    const float a4 = max3(s[12], s[13], s[14]);
+    const float mx = __builtin_elementwise_maximum(max3(a0, a1, a2), max3(a3, a4, s[15]));
     const uint32_t bits = __builtin_bit_cast(uint32_t, mx);
     const auto swapped = __builtin_amdgcn_permlane32_swap(bits, bits, false, false);
-    mx = __builtin_elementwise_maximum(__builtin_bit_cast(float, swapped[0]), __builtin_bit_cast(float, swapped[1]));
-    return mx * c_log2;
+    return __builtin_elementwise_maximum(__builtin_bit_cast(float, swapped[0]), __builtin_bit_cast(float, swapped[1]));
 }
 
-__device__ __forceinline__ bool row_max_update(const f32x16& s, RowState& rs, float& alpha, float c_log2)
+// Lazy base update from a tile's raw row max: the base only moves when some
+// row's max exceeds it by more than 2^8 (the test compares raw scores with
+// the row's threshold, so the common path costs one compare); returns that
+// wave-uniform decision. The caller then rescales l and O by
+// exp2(m_old - m) and refreshes the threshold (finish_rescale).
+__device__ __forceinline__ bool base_update(float mx_raw, RowState& rs, float c_log2)
 {
-    const float mx = row_max_log2(s, c_log2);
-    const bool need = __any(mx > rs.m + kRescaleLog2);
-    const float m_new = need ? __builtin_elementwise_maximum(rs.m, mx) : rs.m;
-    alpha = __builtin_amdgcn_exp2f(rs.m - m_new);  // 1 when the base did not move
-    rs.m = m_new;
-    rs.l *= alpha;
-    return need;
+    const bool moved = __any(mx_raw > rs.thr);
+    if (moved) rs.m = __builtin_elementwise_maximum(rs.m, mx_raw * c_log2);
+    return moved;
 }
 
 template <int D>
@@ -497,6 +500,8 @@ __global__ __launch_bounds__(128 * kWpg) void fused_attention_kernel(const uint1
 
     Frag<D> f;
     RowState rs;
+    const float inv_c = 1.0f / c_log2;
+    rs.thr = (kEmptyBase + kRescaleLog2) * inv_c;
 
     auto run_group = [&](auto gtag) {
         constexpr int G = decltype(gtag)::value;
@@ -604,10 +609,10 @@ __global__ __launch_bounds__(128 * kWpg) void fused_attention_kernel(const uint1
             sbuf[0] = f32x16{};
             qk_part<D, 0, D / 16>(f, ka, sbuf[0]);
             if (tb >= t_mask) mask_tile(sbuf[0], dead_base - tb * kTileKV);
-            float alpha, sum = 0.0f;
-            (void)row_max_update(sbuf[0], rs, alpha, c_log2);  // O is still zero: no rescale
-            exp_part<0, 0, 8>(sbuf[0], p_lo[0], rs.m, c_log2, sum);
-            rs.l += sum;
+            // O and l are still zero: the base moves without rescaling.
+            rs.m = __builtin_elementwise_maximum(rs.m, row_max_raw(sbuf[0]) * c_log2);
+            rs.thr = (rs.m + kRescaleLog2) * inv_c;
+            exp_part<0, 0, 8>(sbuf[0], p_lo[0], rs.m, c_log2, rs.l);
         }
         wait_vm_lgkm0<0>();
         barrier();  // every prologue tile resident; K_0's stage is free
@@ -639,7 +644,6 @@ __global__ __launch_bounds__(128 * kWpg) void fused_attention_kernel(const uint1
             constexpr int P = decltype(par_tag)::value;
             constexpr int B = P & 1;  // S / P register buffer of tile jj
             sbuf[B ^ 1] = f32x16{};
-            float sum = 0.0f;
             static_for<0, kChunk>([&](auto ctag) {
                 constexpr int c = decltype(ctag)::value;
                 qk_part<D, c * kMfmaPer, 1>(f, ka, sbuf[B ^ 1]);
@@ -648,10 +652,9 @@ __global__ __launch_bounds__(128 * kWpg) void fused_attention_kernel(const uint1
                 __builtin_amdgcn_sched_barrier(0);
                 load_v_ops<D, c * kVPer, kVPer>(lds + (P % kStages) * C::kTileElems, f, va);
                 qk_part<D, c * kMfmaPer + 1, kMfmaPer - 1>(f, ka, sbuf[B ^ 1]);
-                exp_part<8 + c * kExpPer, c * kExpPer, kExpPer>(sbuf[B], p_hi, rs.m, c_log2, sum);
+                exp_part<8 + c * kExpPer, c * kExpPer, kExpPer>(sbuf[B], p_hi, rs.m, c_log2, rs.l);
                 __builtin_amdgcn_sched_barrier(0);
             });
-            rs.l += sum;
             pin(p_hi);
             pin(rs.l);
         };
@@ -667,7 +670,8 @@ __global__ __launch_bounds__(128 * kWpg) void fused_attention_kernel(const uint1
                 mask_tile(sbuf[B ^ 1], jj == lw ? -kTileKV : dead_base - t_next * kTileKV);
             __builtin_amdgcn_sched_barrier(0);
             const bf16x8 p_cur[2] = {p_lo[B], p_hi};
-            float alpha, sum = 0.0f;
+            const float m_old = rs.m;
+            float sum = 0.0f;
             bool moved = false;
             static_for<0, kChunk>([&](auto ctag) {
                 constexpr int c = decltype(ctag)::value;
@@ -677,15 +681,25 @@ __global__ __launch_bounds__(128 * kWpg) void fused_attention_kernel(const uint1
                 __builtin_amdgcn_sched_barrier(0);
                 load_k_ops<D, c * kKPer, kKPer>(lds + ((P + 2) % kStages) * C::kTileElems, f, ka);
                 pv_part<D, c * kMfmaPer + 1, kMfmaPer - 1>(f, va, p_cur);
-                if constexpr (c == 0) moved = row_max_update(sbuf[B ^ 1], rs, alpha, c_log2);
+                if constexpr (c == 0) moved = base_update(row_max_raw(sbuf[B ^ 1]), rs, c_log2);
                 exp_part<c * kExpPer, c * kExpPer, kExpPer>(sbuf[B ^ 1], p_lo[B ^ 1], rs.m, c_log2, sum);
                 __builtin_amdgcn_sched_barrier(0);
             });
-            rs.l += sum;
             pin(p_lo[B ^ 1]);
+            pin(sum);
+            if (moved)
+            {
+                // Rare (wave-uniform): sums and O so far used the old base.
+                const float alpha = __builtin_amdgcn_exp2f(m_old - rs.m);
+                rs.l = rs.l * alpha + sum;
+                rs.thr = (rs.m + kRescaleLog2) * inv_c;
+                rescale_o<D>(f, alpha);
+            }
+            else
+            {
+                rs.l += sum;
+            }
             pin(rs.l);
-            pin(alpha);
-            if (moved) rescale_o<D>(f, alpha);
         };
 
         // Steps this wave computes (tiles up to its diagonal / the group's
