@@ -1,0 +1,395 @@
+// Correctness and timing harness for libfa_mi355x, written the way a harness
+// for the reference is written: it includes only include/flash_attention.h,
+// calls cuda_op_lab::flash_attention::* through an entry table, and links
+// the library. It restates the study harness of the reference
+// (benchmarks/bench_flash_attention.cu:391-731) for HIP:
+//   * an accuracy suite on (1,2,256) x head_dim {64,128} x {dense, causal}
+//     with the reference's own inputs (std::mt19937 + normal<float>, seeds
+//     11/22/33, :86-92) checked by the FP64 oracle;
+//   * a timed grid (5 warmups + 30 individually event-timed launches per
+//     kernel, median and IQR from type-7 quantiles, :243-299) over BASELINE's
+//     grid B {1,2,4} x N {512..8192} x D {64,128} x {dense, causal}, H = 8,
+//     uniform[-1,1) inputs reseeded per shape;
+//   * the reference's three CSV files (raw_timings.csv, summary.csv,
+//     accuracy.csv, :419-424) with its column sets; accuracy.csv adds
+//     BASELINE's gate (abs_gate <= 1: |O - O_ref| <= 2^-7 max|O_ref row|).
+// Test infrastructure: the FP64 oracle (oracle/liboracle.so) is the checker.
+//
+// Usage: bench_flash_attention [--quick] [output_directory]
+//   --quick  B = 1, N in {512, 2048} only (eight grid cases).
+// Exit status: 0 when every accuracy row passes both gates and every timed
+// output is finite, 1 otherwise, 2 on a usage or HIP error.
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <filesystem>
+#include <fstream>
+#include <functional>
+#include <iomanip>
+#include <locale>
+#include <string>
+#include <vector>
+
+#include "flash_attention.h"
+#include "oracle.h"
+
+namespace fa = cuda_op_lab::flash_attention;
+
+namespace {
+
+constexpr int kWarmup = 5;
+constexpr int kTimed = 30;
+
+#define HIP_OK(expr)                                                                                       \
+    do                                                                                                     \
+    {                                                                                                      \
+        const hipError_t status_ = (expr);                                                                 \
+        if (status_ != hipSuccess)                                                                         \
+        {                                                                                                  \
+            std::fprintf(stderr, "HIP error %s at %s:%d\n", hipGetErrorString(status_), __FILE__, __LINE__); \
+            std::exit(2);                                                                                  \
+        }                                                                                                  \
+    } while (0)
+
+// One device allocation, freed on scope exit.
+struct DeviceBuffer
+{
+    void* ptr = nullptr;
+    size_t bytes = 0;
+    explicit DeviceBuffer(size_t n) : bytes(n) { HIP_OK(hipMalloc(&ptr, n)); }
+    DeviceBuffer(const DeviceBuffer&) = delete;
+    DeviceBuffer& operator=(const DeviceBuffer&) = delete;
+    ~DeviceBuffer()
+    {
+        if (ptr) (void)hipFree(ptr);
+    }
+    __hip_bfloat16* bf16() const { return static_cast<__hip_bfloat16*>(ptr); }
+};
+
+struct Problem
+{
+    const __hip_bfloat16* q;
+    const __hip_bfloat16* k;
+    const __hip_bfloat16* v;
+    __hip_bfloat16* o;
+    float* workspace;  // v0 only; may be null when its allocation failed
+    fa::AttentionShape shape;
+    bool causal;
+};
+
+// The harness's kernel table (the reference's kEntries, :342-387, plus the
+// v3b slot). Unsupported entries print SKIP, as in the reference.
+struct Entry
+{
+    const char* name;
+    std::function<void(const Problem&)> launch;
+    std::function<bool(int)> supported;
+    std::function<double(const fa::AttentionShape&, bool)> hbm_bytes;  // algorithmic model
+    bool needs_workspace;
+};
+
+double qkvo_bytes(const fa::AttentionShape& s)
+{
+    return 4.0 * s.batch * s.heads * static_cast<double>(s.seq_len) * s.head_dim * 2.0;
+}
+
+std::vector<Entry> entries()
+{
+    return {
+        {"v0_unfused",
+         [](const Problem& p) { fa::launch_attention_unfused(p.q, p.k, p.v, p.o, p.workspace, p.shape, p.causal); },
+         [](int) { return true; },
+         // the reference's model: five fp32 passes over S (:221-231)
+         [](const fa::AttentionShape& s, bool) {
+             return qkvo_bytes(s) + 20.0 * s.batch * s.heads * static_cast<double>(s.seq_len) * s.seq_len;
+         },
+         true},
+        {"v1_fused_row",
+         [](const Problem& p) { fa::launch_attention_fused_row(p.q, p.k, p.v, p.o, p.shape, p.causal); },
+         [](int d) { return fa::fused_row_supported(d); },
+         [](const fa::AttentionShape&, bool) { return 0.0; }, false},
+        {"v2a_fused_tiled",
+         [](const Problem& p) { fa::launch_attention_fusedtiling(p.q, p.k, p.v, p.o, p.shape, p.causal); },
+         [](int d) { return fa::query_fused_tiling(d).supported; },
+         [](const fa::AttentionShape& s, bool c) { return fa::fused_tiling_hbm_bytes(s, c); }, false},
+        {"v2b_fused_tiled",
+         [](const Problem& p) { fa::launch_attention_fusedtiling_v2b(p.q, p.k, p.v, p.o, p.shape, p.causal); },
+         [](int d) { return fa::query_fused_tiling_v2b(d).supported; },
+         [](const fa::AttentionShape& s, bool c) { return fa::fused_tiling_v2b_hbm_bytes(s, c); }, false},
+        {"v3_tensorcore",
+         [](const Problem& p) { fa::launch_attention_tensorcore_v3(p.q, p.k, p.v, p.o, p.shape, p.causal); },
+         [](int d) { return fa::tensorcore_v3_supported(d); },
+         [](const fa::AttentionShape& s, bool c) { return fa::tensorcore_v3_hbm_bytes(s, c); }, false},
+        {"v3b_tensorcore",
+         [](const Problem& p) { fa::launch_attention_tensorcore_v3b(p.q, p.k, p.v, p.o, p.shape, p.causal); },
+         [](int d) { return fa::tensorcore_v3b_supported(d); },
+         [](const fa::AttentionShape& s, bool c) { return fa::tensorcore_v3b_hbm_bytes(s, c); }, false},
+    };
+}
+
+size_t elements(const fa::AttentionShape& s)
+{
+    return static_cast<size_t>(s.batch) * s.heads * s.seq_len * s.head_dim;
+}
+
+// bf16 bit patterns with an all-ones exponent are NaN or Inf.
+void count_nonfinite(const std::vector<uint16_t>& bits, size_t& nan, size_t& inf)
+{
+    nan = inf = 0;
+    for (uint16_t b : bits)
+        if ((b & 0x7f80u) == 0x7f80u) ((b & 0x007fu) ? nan : inf) += 1;
+}
+
+struct Summary
+{
+    std::vector<double> raw;
+    double median = 0, q1 = 0, q3 = 0;
+};
+
+// Each sample brackets one launch (all of v0's kernels) with events on the
+// null stream and waits for it, as the reference's time_iterations does.
+Summary time_entry(const Entry& e, const Problem& p)
+{
+    for (int i = 0; i < kWarmup; ++i) e.launch(p);
+    HIP_OK(hipGetLastError());
+    HIP_OK(hipDeviceSynchronize());
+    hipEvent_t start, stop;
+    HIP_OK(hipEventCreate(&start));
+    HIP_OK(hipEventCreate(&stop));
+    Summary s;
+    for (int i = 0; i < kTimed; ++i)
+    {
+        HIP_OK(hipEventRecord(start, nullptr));
+        e.launch(p);
+        HIP_OK(hipEventRecord(stop, nullptr));
+        HIP_OK(hipGetLastError());
+        HIP_OK(hipEventSynchronize(stop));
+        float ms = 0.0f;
+        HIP_OK(hipEventElapsedTime(&ms, start, stop));
+        if (!std::isfinite(ms) || ms <= 0.0f)
+        {
+            std::fprintf(stderr, "invalid event timing %g ms\n", ms);
+            std::exit(2);
+        }
+        s.raw.push_back(ms);
+    }
+    HIP_OK(hipEventDestroy(start));
+    HIP_OK(hipEventDestroy(stop));
+    std::vector<double> sorted = s.raw;
+    std::sort(sorted.begin(), sorted.end());
+    s.median = fa_oracle_quantile_sorted(sorted.data(), static_cast<int64_t>(sorted.size()), 0.5);
+    s.q1 = fa_oracle_quantile_sorted(sorted.data(), static_cast<int64_t>(sorted.size()), 0.25);
+    s.q3 = fa_oracle_quantile_sorted(sorted.data(), static_cast<int64_t>(sorted.size()), 0.75);
+    return s;
+}
+
+std::ofstream open_csv(const std::filesystem::path& path, const char* header)
+{
+    std::ofstream f(path);
+    if (!f)
+    {
+        std::fprintf(stderr, "cannot open %s\n", path.string().c_str());
+        std::exit(2);
+    }
+    f.imbue(std::locale::classic());
+    f << std::setprecision(17) << header << '\n';
+    return f;
+}
+
+void key(std::ostream& f, const char* name, const fa::AttentionShape& s, bool causal)
+{
+    f << name << ',' << s.batch << ',' << s.heads << ',' << s.seq_len << ',' << s.head_dim << ',' << (causal ? 1 : 0);
+}
+
+// Per-shape seeds of the grid, the same as tests/test_gpu_grid.py uses.
+uint64_t grid_seed(uint64_t tensor_seed, const fa::AttentionShape& s)
+{
+    return tensor_seed + 1000ull * s.batch + 10ull * (s.seq_len / 512) + s.head_dim;
+}
+
+}  // namespace
+
+int main(int argc, char** argv)
+{
+    bool quick = false;
+    std::filesystem::path out_dir = "results/raw/flash_attention";
+    for (int a = 1; a < argc; ++a)
+    {
+        const std::string arg = argv[a];
+        if (arg == "--quick") quick = true;
+        else if (arg == "--help" || arg == "-h")
+        {
+            std::printf("usage: %s [--quick] [output_directory]\n", argv[0]);
+            return 0;
+        }
+        else out_dir = arg;
+    }
+    std::error_code ec;
+    std::filesystem::create_directories(out_dir, ec);
+    if (ec)
+    {
+        std::fprintf(stderr, "cannot create %s: %s\n", out_dir.string().c_str(), ec.message().c_str());
+        return 2;
+    }
+    auto raw_csv = open_csv(out_dir / "raw_timings.csv", "kernel,batch,heads,seq_len,head_dim,causal,iteration,elapsed_ms");
+    auto summary_csv = open_csv(out_dir / "summary.csv",
+                                "kernel,batch,heads,seq_len,head_dim,causal,status,warmup_iters,timed_iters,"
+                                "median_ms,q1_ms,q3_ms,iqr_ms,baseline_median_ms,speedup_vs_v0,"
+                                "tflops,algorithmic_hbm_gb,v0_workspace_bytes,output_nan,output_inf");
+    auto accuracy_csv = open_csv(out_dir / "accuracy.csv",
+                                 "kernel,batch,heads,seq_len,head_dim,causal,vs_double,row_scaled_error,"
+                                 "max_abs_error,row_scale_ulp,output_nan,output_inf,reference_nan,reference_inf,"
+                                 "passed,abs_gate");
+
+    hipDeviceProp_t props{};
+    HIP_OK(hipGetDeviceProperties(&props, 0));
+    std::printf("device: %s (%s, %d CUs)\n", props.name, props.gcnArchName, props.multiProcessorCount);
+    std::printf("timing: %d warmups, %d individually event-timed launches; median and IQR\n\n", kWarmup, kTimed);
+
+    std::printf("fused kernel resources:\n  %-14s %8s %6s %8s %8s %12s %6s %7s %10s\n", "kernel", "head_dim", "block",
+                "tile_kv", "q_rows", "shared/block", "regs", "local", "blocks/CU");
+    for (int d : {64, 128})
+        for (const auto& [name, info] : {std::pair{"v3_tensorcore", fa::query_tensorcore_v3(d)},
+                                         std::pair{"v3b_tensorcore", fa::query_tensorcore_v3b(d)}})
+            std::printf("  %-14s %8d %6d %8d %8d %11dB %6d %6dB %10d\n", name, d, info.block_size, info.tile_kv,
+                        info.rows_per_block, info.shared_bytes_per_block, info.registers_per_thread,
+                        info.local_bytes_per_thread, info.max_blocks_per_sm);
+    std::printf("\n");
+
+    const std::vector<Entry> table = entries();
+    bool all_ok = true;
+
+    // Accuracy suite: the reference's shape and inputs.
+    std::printf("accuracy (1,2,256), reference inputs:\n  %-16s %5s %6s %11s %11s %11s %7s %8s %6s\n", "kernel", "D",
+                "causal", "vs_double", "row_scaled", "max_abs", "ulp", "abs_gate", "status");
+    for (int d : {64, 128})
+        for (bool causal : {false, true})
+        {
+            const fa::AttentionShape s{1, 2, 256, d};
+            const size_t n = elements(s);
+            std::vector<uint16_t> hq(n), hk(n), hv(n), ho(n);
+            fa_oracle_fill_normal_mt19937(hq.data(), static_cast<int64_t>(n), 11u);
+            fa_oracle_fill_normal_mt19937(hk.data(), static_cast<int64_t>(n), 22u);
+            fa_oracle_fill_normal_mt19937(hv.data(), static_cast<int64_t>(n), 33u);
+            std::vector<double> ref(n);
+            if (fa_oracle_attention(hq.data(), hk.data(), hv.data(), ref.data(), s.batch, s.heads, s.seq_len, d,
+                                    causal ? 1 : 0, nullptr, 0, 0) != 0)
+                return 2;
+            DeviceBuffer q(n * 2), k(n * 2), v(n * 2), o(n * 2), ws(fa::unfused_workspace_bytes(s));
+            HIP_OK(hipMemcpy(q.ptr, hq.data(), n * 2, hipMemcpyHostToDevice));
+            HIP_OK(hipMemcpy(k.ptr, hk.data(), n * 2, hipMemcpyHostToDevice));
+            HIP_OK(hipMemcpy(v.ptr, hv.data(), n * 2, hipMemcpyHostToDevice));
+            const Problem p{q.bf16(), k.bf16(), v.bf16(), o.bf16(), static_cast<float*>(ws.ptr), s, causal};
+            for (const Entry& e : table)
+            {
+                if (!e.supported(d)) continue;
+                HIP_OK(hipMemset(o.ptr, 0xff, n * 2));  // unwritten outputs read as NaN
+                e.launch(p);
+                HIP_OK(hipGetLastError());
+                HIP_OK(hipDeviceSynchronize());
+                HIP_OK(hipMemcpy(ho.data(), o.ptr, n * 2, hipMemcpyDeviceToHost));
+                fa_oracle_accuracy acc{};
+                fa_oracle_compare(ho.data(), ref.data(), static_cast<int64_t>(n / d), d, &acc);
+                const bool ok = acc.passed_ulp && acc.passed_abs;
+                all_ok = all_ok && ok;
+                std::printf("  %-16s %5d %6s %11.4e %11.4e %11.4e %7.2f %8.3f %6s\n", e.name, d, causal ? "yes" : "no",
+                            acc.vs_double, acc.row_scaled, acc.max_abs, acc.ulp, acc.abs_gate, ok ? "PASS" : "FAIL");
+                key(accuracy_csv, e.name, s, causal);
+                accuracy_csv << ',' << acc.vs_double << ',' << acc.row_scaled << ',' << acc.max_abs << ',' << acc.ulp
+                             << ',' << acc.output_nan << ',' << acc.output_inf << ',' << acc.reference_nan << ','
+                             << acc.reference_inf << ',' << (ok ? 1 : 0) << ',' << acc.abs_gate << '\n';
+            }
+        }
+    accuracy_csv.flush();
+    std::printf("\n");
+
+    // Timed grid.
+    std::vector<int> batches = {1, 2, 4}, lengths = {512, 1024, 2048, 4096, 8192};
+    if (quick)
+    {
+        batches = {1};
+        lengths = {512, 2048};
+    }
+    size_t skipped = 0;
+    for (int b : batches)
+        for (int nlen : lengths)
+            for (int d : {64, 128})
+                for (bool causal : {false, true})
+                {
+                    const fa::AttentionShape s{b, 8, nlen, d};
+                    const size_t n = elements(s);
+                    std::vector<uint16_t> host(n);
+                    DeviceBuffer q(n * 2), k(n * 2), v(n * 2), o(n * 2);
+                    fa_oracle_fill_uniform(host.data(), static_cast<int64_t>(n), grid_seed(11, s));
+                    HIP_OK(hipMemcpy(q.ptr, host.data(), n * 2, hipMemcpyHostToDevice));
+                    fa_oracle_fill_uniform(host.data(), static_cast<int64_t>(n), grid_seed(22, s));
+                    HIP_OK(hipMemcpy(k.ptr, host.data(), n * 2, hipMemcpyHostToDevice));
+                    fa_oracle_fill_uniform(host.data(), static_cast<int64_t>(n), grid_seed(33, s));
+                    HIP_OK(hipMemcpy(v.ptr, host.data(), n * 2, hipMemcpyHostToDevice));
+                    const size_t ws_bytes = fa::unfused_workspace_bytes(s);
+                    void* ws = nullptr;
+                    const bool have_ws = hipMalloc(&ws, ws_bytes) == hipSuccess;
+                    if (!have_ws) (void)hipGetLastError();
+                    const Problem p{q.bf16(), k.bf16(), v.bf16(), o.bf16(), static_cast<float*>(ws), s, causal};
+                    // 4*B*H*N^2*D, halved for causal (BASELINE's convention)
+                    const double flops = 4.0 * b * s.heads * static_cast<double>(nlen) * nlen * d * (causal ? 0.5 : 1.0);
+                    std::printf("B=%d H=8 N=%d D=%d %s\n  %-16s %10s %10s %9s %9s %9s\n", b, nlen, d,
+                                causal ? "causal" : "dense", "kernel", "median ms", "IQR ms", "TFLOPS", "HBM GB",
+                                "speedup");
+                    double baseline_ms = 0.0;
+                    for (const Entry& e : table)
+                    {
+                        const double gb = e.hbm_bytes(s, causal) / 1e9;
+                        const char* skip = !e.supported(d) ? "unsupported"
+                                           : (e.needs_workspace && !have_ws ? "workspace_allocation_failed" : nullptr);
+                        if (skip)
+                        {
+                            ++skipped;
+                            std::printf("  %-16s SKIP (%s)\n", e.name, skip);
+                            key(summary_csv, e.name, s, causal);
+                            summary_csv << ',' << skip << ",0,0,,,,,,,," << gb << ',' << ws_bytes << ",,\n";
+                            continue;
+                        }
+                        HIP_OK(hipMemset(o.ptr, 0xff, n * 2));
+                        const Summary t = time_entry(e, p);
+                        std::vector<uint16_t> out(n);
+                        HIP_OK(hipMemcpy(out.data(), o.ptr, n * 2, hipMemcpyDeviceToHost));
+                        size_t nan = 0, inf = 0;
+                        count_nonfinite(out, nan, inf);
+                        const bool finite = nan == 0 && inf == 0;
+                        all_ok = all_ok && finite;
+                        if (std::strcmp(e.name, "v0_unfused") == 0 && finite) baseline_ms = t.median;
+                        const double tflops = flops / (t.median * 1e-3) / 1e12;
+                        const bool have_speedup = baseline_ms > 0.0 && finite;
+                        std::printf("  %-16s %10.4f %10.4f %9.1f %9.3f", e.name, t.median, t.q3 - t.q1, tflops, gb);
+                        if (have_speedup) std::printf(" %8.2fx", baseline_ms / t.median);
+                        std::printf("%s\n", finite ? "" : "  NONFINITE");
+                        for (size_t it = 0; it < t.raw.size(); ++it)
+                        {
+                            key(raw_csv, e.name, s, causal);
+                            raw_csv << ',' << it + 1 << ',' << t.raw[it] << '\n';
+                        }
+                        key(summary_csv, e.name, s, causal);
+                        summary_csv << ',' << (finite ? "ok" : "nonfinite_output") << ',' << kWarmup << ','
+                                    << t.raw.size() << ',' << t.median << ',' << t.q1 << ',' << t.q3 << ','
+                                    << t.q3 - t.q1 << ',';
+                        if (baseline_ms > 0.0) summary_csv << baseline_ms;
+                        summary_csv << ',';
+                        if (have_speedup) summary_csv << baseline_ms / t.median;
+                        summary_csv << ',' << tflops << ',' << gb << ',' << ws_bytes << ',' << nan << ',' << inf << '\n';
+                    }
+                    if (ws) HIP_OK(hipFree(ws));
+                    raw_csv.flush();
+                    summary_csv.flush();
+                }
+    std::printf("\n%s; %zu kernel/shape runs skipped; CSV files in %s\n",
+                all_ok ? "all accuracy rows passed and all timed outputs are finite" : "FAILED", skipped,
+                out_dir.string().c_str());
+    return all_ok ? 0 : 1;
+}

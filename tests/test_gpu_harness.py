@@ -1,0 +1,62 @@
+"""The C++ harness (tests/harness/bench_flash_attention.cpp), a consumer of
+include/flash_attention.h in the shape of the reference's study harness
+(benchmarks/bench_flash_attention.cu:391-731), run on the GPU in --quick
+mode: its accuracy suite must pass both gates for every supported kernel, its
+timed outputs must be finite, and its three CSV files must carry the
+reference's column sets (:419-424), so the reference's plotting reads them.
+"""
+import csv
+import os
+import subprocess
+
+import pytest
+
+pytestmark = pytest.mark.gpu
+HERE = os.path.dirname(os.path.abspath(__file__))
+BINARY = os.path.join(HERE, "harness", "bench_flash_attention")
+
+RAW = "kernel,batch,heads,seq_len,head_dim,causal,iteration,elapsed_ms".split(",")
+SUMMARY = ("kernel,batch,heads,seq_len,head_dim,causal,status,warmup_iters,timed_iters,median_ms,q1_ms,q3_ms,"
+           "iqr_ms,baseline_median_ms,speedup_vs_v0,tflops,algorithmic_hbm_gb,v0_workspace_bytes,output_nan,"
+           "output_inf").split(",")
+ACCURACY = ("kernel,batch,heads,seq_len,head_dim,causal,vs_double,row_scaled_error,max_abs_error,row_scale_ulp,"
+            "output_nan,output_inf,reference_nan,reference_inf,passed").split(",")
+
+
+def rows(path):
+    with open(path, newline="") as fh:
+        reader = csv.DictReader(fh)
+        return reader.fieldnames, list(reader)
+
+
+def test_harness_quick(tmp_path):
+    if not os.path.exists(BINARY):
+        pytest.fail(f"{BINARY} is missing: run __graft_entry__.build()")
+    print("harness --quick", flush=True)
+    run = subprocess.run([BINARY, "--quick", str(tmp_path)], capture_output=True, text=True, timeout=300)
+    assert run.returncode == 0, run.stdout[-3000:] + run.stderr[-2000:]
+
+    fields, acc = rows(tmp_path / "accuracy.csv")
+    assert fields[:len(ACCURACY)] == ACCURACY and fields[-1] == "abs_gate"
+    kernels = {r["kernel"] for r in acc}
+    assert kernels == {"v0_unfused", "v3_tensorcore", "v3b_tensorcore"}
+    assert len(acc) == 3 * 2 * 2  # kernels x head_dim x mask
+    for r in acc:
+        assert r["passed"] == "1" and float(r["row_scale_ulp"]) <= 2.0 and float(r["abs_gate"]) <= 1.0, r
+
+    fields, summ = rows(tmp_path / "summary.csv")
+    assert fields == SUMMARY
+    assert len(summ) == 8 * 6  # 8 quick cases x 6 entries
+    for r in summ:
+        if r["kernel"] in ("v1_fused_row", "v2a_fused_tiled", "v2b_fused_tiled"):
+            assert r["status"] == "unsupported"
+            continue
+        assert r["status"] == "ok" and r["output_nan"] == "0" and r["output_inf"] == "0", r
+        q1, med, q3 = float(r["q1_ms"]), float(r["median_ms"]), float(r["q3_ms"])
+        assert 0 < q1 <= med <= q3
+        if r["kernel"] != "v0_unfused":
+            assert float(r["speedup_vs_v0"]) > 1.0, r
+
+    fields, raw = rows(tmp_path / "raw_timings.csv")
+    assert fields == RAW
+    assert len(raw) == 8 * 3 * 30
