@@ -424,6 +424,7 @@ __global__ __launch_bounds__(128 * kWpg) void fused_attention_kernel(const uint1
     // the Q rows of the workgroup's slots follow.
     __shared__ __attribute__((aligned(16))) uint16_t lds[C::kLdsElems + C::kQElems];
 
+    const uint32_t lds_base = lds_addr(lds);  // LDS byte address of the array
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -506,7 +507,10 @@ __global__ __launch_bounds__(128 * kWpg) void fused_attention_kernel(const uint1
     auto run_group = [&](auto gtag) {
         constexpr int G = decltype(gtag)::value;
         uint16_t* const kb = lds + G * C::kGroupElems;            // K stages of this group
-        uint16_t* const vb = kb + kStages * C::kTileElems;        // V stages of this group
+        // LDS byte addresses of this group's K and V stages (DMA targets):
+        // the array's base plus compile-time offsets.
+        const uint32_t k_lds = lds_base + G * C::kGroupElems * 2;
+        const uint32_t v_lds = k_lds + kStages * C::kTileElems * 2;
         const int tb = G == 0 ? 0 : split.first1;                 // first tile of this group
         const int cnt = G == 0 ? split.count0 : split.count1;
         const int lw = min(cnt - 1, t_last - tb);                 // last local tile this wave computes
@@ -520,10 +524,10 @@ __global__ __launch_bounds__(128 * kWpg) void fused_attention_kernel(const uint1
         dma_lane_offsets<D, kWpg, true>(wg, lane, voff);
         auto kv_at = [&](int jj) { return min(tb + jj, n_tiles - 1) * kTileKV; };
         auto copy_k = [&](int jj, int stage, int u) {
-            dma_copy<D, kWpg>(tile_rsrc<D>(k_bytes, kv_at(jj), n), lds_addr(kb + stage * C::kTileElems), wg_s, u, koff);
+            dma_copy<D, kWpg>(tile_rsrc<D>(k_bytes, kv_at(jj), n), k_lds + stage * (C::kTileElems * 2), wg_s, u, koff);
         };
         auto copy_v = [&](int jj, int stage, int u) {
-            dma_copy<D, kWpg>(tile_rsrc<D>(v_bytes, kv_at(jj), n), lds_addr(vb + stage * C::kTileElems), wg_s, u, voff);
+            dma_copy<D, kWpg>(tile_rsrc<D>(v_bytes, kv_at(jj), n), v_lds + stage * (C::kTileElems * 2), wg_s, u, voff);
         };
 
         // Prologue: the wave's Q rows first, then K_0 .. K_{S-1},
@@ -549,7 +553,7 @@ __global__ __launch_bounds__(128 * kWpg) void fused_attention_kernel(const uint1
                 const uint32_t voff = static_cast<uint32_t>(row * (D * 2) + ((pchunk ^ swz_k<D>(row)) * 16));
                 const uint32_t bytes = row0 < n ? static_cast<uint32_t>((n - row0) * (D * 2)) : 0u;
                 const i32x4 rsrc = make_rsrc(q_bytes, static_cast<uint32_t>(min(row0, n) * (D * 2)), bytes);
-                dma16(rsrc, voff, lds_addr(lds + C::kLdsElems + qs * 32 * D) + u * 1024);
+                dma16(rsrc, voff, lds_base + (C::kLdsElems + qs * 32 * D) * 2 + u * 1024);
             }
         }
 #pragma unroll
