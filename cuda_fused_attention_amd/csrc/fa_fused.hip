@@ -34,7 +34,8 @@
 //                (the step's only one);
 //       block B: the K operands of tile jj+2 are read; the MFMA pipe
 //                accumulates O^T += V^T P^T of tile jj while the VALU starts
-//                tile jj+1 (mask, row max, first half of the exponentials);
+//                tile jj+1 (mask, first half of the exponentials) after
+//                checking tile jj's row sums;
 //                the wave issues its share of the copies of V tile jj+3.
 //     MFMA and VALU work of one wave are independent inside each block, so
 //     the compiler interleaves them within each chunk (scheduling fences
@@ -50,10 +51,12 @@
 //     sequence end read as zero (and are masked). Descriptor arithmetic is
 //     scalar: slab bases and tile indices are wave-uniform.
 //   * Scores stay in the log2 domain (scale*log2(e) folded into one FMA before
-//     v_exp_f32). The exponent base (running max) is only raised when a row's
-//     max grows by more than 2^8, then O and the row sum are rescaled; P stays
-//     <= 256. Row sums accumulate the bf16-rounded P with v_dot2_f32_bf16, the
-//     same weights the PV MFMA uses.
+//     v_exp_f32). Row sums accumulate the bf16-rounded P with
+//     v_dot2_f32_bf16, the same weights the PV MFMA uses. The exponent base
+//     is set from the first tile's row max; afterwards no per-tile row max is
+//     taken: the base is raised only when a tile's partial row sum exceeds
+//     2^8, and then O and the row sum are rescaled and the tile recomputed.
+//     Every P the matrix pipe consumes is <= 256.
 //   * Causal: a wave skips tiles wholly above its diagonal, and only tiles
 //     that cross the diagonal or the sequence end pay for the per-element
 //     mask (-inf). A workgroup owns two half blocks of rows, an early one and
@@ -86,7 +89,7 @@ typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
 constexpr int kTileKV = fa::kFusedTileKV;  // keys per LDS tile
 constexpr int kStages = fa::kFusedStages;  // LDS stages per tensor per group
-constexpr float kRescaleLog2 = 8.0f;       // raise the exponent base when a row max grows by > 2^8
+constexpr float kSumLimit = 256.0f;        // a tile's partial row sum above this moves the exponent base
 
 template <int D, int kWpg>
 struct Cfg
@@ -338,7 +341,6 @@ constexpr float kEmptyBase = -1.0e30f;
 struct RowState
 {
     float m = kEmptyBase;  // exponent base, log2 domain, wave-lazily raised
-    float thr;             // raw score above which the base must move: (m + kRescaleLog2) / c_log2
     float l = 0.0f;        // partial row sum of the bf16-rounded P
 };
 
@@ -387,18 +389,6 @@ __device__ __forceinline__ float row_max_raw(const f32x16& s)
     const uint32_t bits = __builtin_bit_cast(uint32_t, mx);
     const auto swapped = __builtin_amdgcn_permlane32_swap(bits, bits, false, false);
     return __builtin_elementwise_maximum(__builtin_bit_cast(float, swapped[0]), __builtin_bit_cast(float, swapped[1]));
-}
-
-// Lazy base update from a tile's raw row max: the base only moves when some
-// row's max exceeds it by more than 2^8 (the test compares raw scores with
-// the row's threshold, so the common path costs one compare); returns that
-// wave-uniform decision. The caller then rescales l and O by
-// exp2(m_old - m) and refreshes the threshold (finish_rescale).
-__device__ __forceinline__ bool base_update(float mx_raw, RowState& rs, float c_log2)
-{
-    const bool moved = __any(mx_raw > rs.thr);
-    if (moved) rs.m = __builtin_elementwise_maximum(rs.m, mx_raw * c_log2);
-    return moved;
 }
 
 template <int D>
@@ -501,8 +491,6 @@ __global__ __launch_bounds__(128 * kWpg) void fused_attention_kernel(const uint1
 
     Frag<D> f;
     RowState rs;
-    const float inv_c = 1.0f / c_log2;
-    rs.thr = (kEmptyBase + kRescaleLog2) * inv_c;
 
     auto run_group = [&](auto gtag) {
         constexpr int G = decltype(gtag)::value;
@@ -607,6 +595,7 @@ __global__ __launch_bounds__(128 * kWpg) void fused_attention_kernel(const uint1
         bf16x8 p_hi;
         bf16x8 ka[D / 16];
         bf16x8 va[D / 32][2];
+        float tsum = 0.0f;  // partial row sum of the tile being exponentiated
         if (lw >= 0)
         {
             load_k_ops<D>(lds, f, ka);
@@ -615,8 +604,7 @@ __global__ __launch_bounds__(128 * kWpg) void fused_attention_kernel(const uint1
             if (tb >= t_mask) mask_tile(sbuf[0], dead_base - tb * kTileKV);
             // O and l are still zero: the base moves without rescaling.
             rs.m = __builtin_elementwise_maximum(rs.m, row_max_raw(sbuf[0]) * c_log2);
-            rs.thr = (rs.m + kRescaleLog2) * inv_c;
-            exp_part<0, 0, 8>(sbuf[0], p_lo[0], rs.m, c_log2, rs.l);
+            exp_part<0, 0, 8>(sbuf[0], p_lo[0], rs.m, c_log2, tsum);
         }
         wait_vm_lgkm0<0>();
         barrier();  // every prologue tile resident; K_0's stage is free
@@ -634,9 +622,55 @@ __global__ __launch_bounds__(128 * kWpg) void fused_attention_kernel(const uint1
         //   Block A: V operand reads of tile jj; copies of K tile jj+4;
         //            S^T of tile jj+1 beside the second half of tile jj's
         //            exponentials.
-        //   Block B: K operand reads of tile jj+2; copies of V tile jj+3;
-        //            O^T += V^T P^T of tile jj beside tile jj+1's row max and
-        //            the first half of its exponentials.
+        //   Block B: the check of tile jj's row sums; K operand reads of
+        //            tile jj+2; copies of V tile jj+3; O^T += V^T P^T of tile
+        //            jj beside the first half of tile jj+1's exponentials.
+        //
+        // Exponentials use the current base; no per-tile row max is taken.
+        // Every P is at most its tile's partial row sum (P >= 0), so a sum
+        // <= kSumLimit bounds every P of the tile. A larger (or infinite) sum
+        // means the base lags the row max. Then (rare, wave-uniform) the
+        // tile's P is zeroed before the matrix pipe consumes it, and after
+        // block B's products the wave recomputes the tile's scores from K
+        // re-read from global memory (its stage is already being refilled),
+        // moves the base to the row max, rescales l and O, accumulates the
+        // tile's P V^T again from V's stage (still intact until the next
+        // step's copies) and redoes the first half of tile jj+1's
+        // exponentials. NaN scores give NaN sums, which fail the test and
+        // propagate to the output. The check runs after the step's barrier,
+        // by when the row-sum chain has drained.
+        const uint16_t* const k_slab = k + slab_off;
+        auto rebase = [&](auto par_tag, int jj) {
+            constexpr int P = decltype(par_tag)::value;
+            constexpr int B = P & 1;
+            const int t = tb + jj;
+            const int key = t * kTileKV + i;
+            // One K operand at a time (the path is rare; registers are not).
+            f32x16 st = {};
+#pragma unroll
+            for (int ks = 0; ks < D / 16; ++ks)
+            {
+                const bf16x8 kr = key < n ? *reinterpret_cast<const bf16x8*>(k_slab + static_cast<size_t>(key) * D +
+                                                                              (2 * ks + h) * 8)
+                                          : bf16x8{};
+                st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kr, f.q[ks], st, 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            if (t >= t_mask) mask_tile(st, dead_base - t * kTileKV);
+            const float m_new = __builtin_elementwise_maximum(rs.m, row_max_raw(st) * c_log2);
+            const float alpha = __builtin_amdgcn_exp2f(rs.m - m_new);
+            rs.m = m_new;
+            rescale_o<D>(f, alpha);
+            float sum = 0.0f;
+            bf16x8 pr[2];
+            exp_part<0, 0, 8>(st, pr[0], rs.m, c_log2, sum);
+            exp_part<8, 0, 8>(st, pr[1], rs.m, c_log2, sum);
+            rs.l = rs.l * alpha + sum;
+            load_v_ops<D>(lds + (P % kStages) * C::kTileElems, f, va);
+            pv_part<D, 0, D / 16>(f, va, pr);
+            tsum = 0.0f;
+            exp_part<0, 0, 8>(sbuf[B ^ 1], p_lo[B ^ 1], rs.m, c_log2, tsum);
+        };
         constexpr int kChunk = C::kIssues;            // chunks per block
         constexpr int kMfmaPer = (D / 16) / kChunk;   // MFMAs per chunk
         constexpr int kExpPer = 8 / kChunk;           // exponentials per chunk
@@ -656,27 +690,36 @@ __global__ __launch_bounds__(128 * kWpg) void fused_attention_kernel(const uint1
                 __builtin_amdgcn_sched_barrier(0);
                 load_v_ops<D, c * kVPer, kVPer>(lds + (P % kStages) * C::kTileElems, f, va);
                 qk_part<D, c * kMfmaPer + 1, kMfmaPer - 1>(f, ka, sbuf[B ^ 1]);
-                exp_part<8 + c * kExpPer, c * kExpPer, kExpPer>(sbuf[B], p_hi, rs.m, c_log2, rs.l);
+                exp_part<8 + c * kExpPer, c * kExpPer, kExpPer>(sbuf[B], p_hi, rs.m, c_log2, tsum);
                 __builtin_amdgcn_sched_barrier(0);
             });
             pin(p_hi);
-            pin(rs.l);
+            pin(tsum);
         };
         auto block_b = [&](auto par_tag, int jj) {
             constexpr int P = decltype(par_tag)::value;
             constexpr int B = P & 1;
-            // Diagonal / tail tile (uniform, rare): mask before the row max.
-            // On the wave's last tile (jj == lw) the "next" S^T is a dummy
-            // product with a landed stage: masking all of it makes the head a
-            // no-op (max -inf, base unmoved, P = 0).
+            const bool rare = __any(tsum > kSumLimit);
+            if (rare)
+            {
+                // The empty volatile asm keeps this a branch (not selects on
+                // the common path).
+                asm volatile("");
+                p_lo[B] = bf16x8{};
+                p_hi = bf16x8{};
+                tsum = 0.0f;
+            }
+            rs.l += tsum;
+            // Diagonal / tail tile (uniform, rare): mask before the
+            // exponentials. On the wave's last tile (jj == lw) the "next" S^T
+            // is a dummy product with a landed stage: masking all of it makes
+            // its P and sums zero.
             const int t_next = tb + jj + 1;
             if (t_next >= t_mask || jj == lw)
                 mask_tile(sbuf[B ^ 1], jj == lw ? -kTileKV : dead_base - t_next * kTileKV);
             __builtin_amdgcn_sched_barrier(0);
             const bf16x8 p_cur[2] = {p_lo[B], p_hi};
-            const float m_old = rs.m;
-            float sum = 0.0f;
-            bool moved = false;
+            tsum = 0.0f;
             static_for<0, kChunk>([&](auto ctag) {
                 constexpr int c = decltype(ctag)::value;
                 pv_part<D, c * kMfmaPer, 1>(f, va, p_cur);
@@ -685,24 +728,12 @@ __global__ __launch_bounds__(128 * kWpg) void fused_attention_kernel(const uint1
                 __builtin_amdgcn_sched_barrier(0);
                 load_k_ops<D, c * kKPer, kKPer>(lds + ((P + 2) % kStages) * C::kTileElems, f, ka);
                 pv_part<D, c * kMfmaPer + 1, kMfmaPer - 1>(f, va, p_cur);
-                if constexpr (c == 0) moved = base_update(row_max_raw(sbuf[B ^ 1]), rs, c_log2);
-                exp_part<c * kExpPer, c * kExpPer, kExpPer>(sbuf[B ^ 1], p_lo[B ^ 1], rs.m, c_log2, sum);
+                exp_part<c * kExpPer, c * kExpPer, kExpPer>(sbuf[B ^ 1], p_lo[B ^ 1], rs.m, c_log2, tsum);
                 __builtin_amdgcn_sched_barrier(0);
             });
             pin(p_lo[B ^ 1]);
-            pin(sum);
-            if (moved)
-            {
-                // Rare (wave-uniform): sums and O so far used the old base.
-                const float alpha = __builtin_amdgcn_exp2f(m_old - rs.m);
-                rs.l = rs.l * alpha + sum;
-                rs.thr = (rs.m + kRescaleLog2) * inv_c;
-                rescale_o<D>(f, alpha);
-            }
-            else
-            {
-                rs.l += sum;
-            }
+            pin(tsum);
+            if (rare) rebase(par_tag, jj);
             pin(rs.l);
         };
 

@@ -23,10 +23,13 @@ constexpr int kFusedStages = 4;   // LDS stages per tensor (K, V) per wave group
 //            jj + kFusedKAhead (its copies spread between the MFMAs);
 //   barrier  wait until only the DMAs of steps jj-1 and jj are in flight and
 //            every LDS read issued so far has completed; workgroup barrier;
-//   block B  read the K operands of tile jj + 2; DMA V tile jj + kFusedVAhead.
+//   block B  read the K operands of tile jj + 2; DMA V tile jj + kFusedVAhead;
+//            rarely (an exponent-base move), read tile jj's V operands
+//            again at the end of the block.
 // One barrier per step covers both hazards: K_{jj+2} and V_{jj+1} landed
 // before it (read after it), and every stage a later copy overwrites was
-// last read before it or before the previous step's barrier.
+// last read before it or before the previous step's barrier (V_{jj-1}'s
+// stage, the target of block B's copy, was last read in step jj - 1).
 // The prologue copies K_0 .. K_3 and V_0 .. V_2, waits for K_0 and reads
 // its operands, then waits for every prologue copy and reads K_1's operands.
 constexpr int kFusedKAhead = kFusedStages;      // into K_jj's stage (read in step jj - 2)

@@ -16,7 +16,9 @@ per-step actions and checks, for every tile count:
       for (the model's waits are the kernel's vmcnt waits: all copy groups but
       the last n issued have landed) and a barrier passed, and no DMA targets
       a stage whose tile is still to be read (so every read sees the tile it
-      expects).
+      expects). The model always takes the rare base-move fix-up at the end
+      of block B, which re-reads tile jj's V stage after the step's barrier:
+      that stage is free only after the next step's barrier.
 """
 import os
 import subprocess
@@ -80,7 +82,7 @@ int main() {
             // A stage is free once its reads are followed by a barrier:
             // K_0 was read before the second prologue barrier; K_1 is read
             // after it and freed by step 0's barrier.
-            int k_consumed = 0, k_pending = 1, v_consumed = -1;
+            int k_consumed = 0, k_pending = 1, v_consumed = -1, v_pending = -1;
             int steps = 0;
             fused_group_walk(cnt, [&](auto par, int jj) {
                 ++steps;
@@ -92,12 +94,15 @@ int main() {
                 // still fly; every LDS read issued so far has completed
                 wait_allow(3);
                 barrier(); ++barriers;
-                v_consumed = jj;
+                v_consumed = v_pending;
                 k_consumed = k_pending;
                 // block B: K operands of tile jj+2; copies of V tile jj+VAhead
                 if (jj + 2 < cnt) read(ks, (jj + 2) % S, jj + 2);
                 k_pending = jj + 2;
                 dma(vs, (jj + kFusedVAhead) % S, jj + kFusedVAhead, v_consumed);
+                // end of block B, base-move fix-up: V operands of tile jj again
+                read(vs, jj % S, jj);
+                v_pending = jj;
             });
             if (steps != cnt) ++bad;
             if (barriers != fused_group_barriers(g, cnt)) ++bad;
@@ -123,19 +128,28 @@ def test_schedule_barriers_and_stages(tmp_path):
 
 def test_schedule_checker_catches_a_short_pipeline(tmp_path):
     """Planted mistakes: a K prefetch two tiles further ahead overwrites a
-    stage still to be read; a mid-step wait that lets one more copy group fly,
-    and a prologue wait that lets the last prologue copies fly, read a stage
-    before its copy landed. The checker must report each."""
+    stage still to be read; V copies one tile further ahead (with a fourth
+    prologue V copy, so every other read still finds its tile) overwrite the
+    stage the base-move fix-up re-reads after the barrier; a mid-step wait
+    that lets one more copy group fly, and a prologue wait that lets the last
+    prologue copies fly, read a stage before its copy landed. The checker must
+    report each."""
     plants = [
-        ("dma(ks, (jj + kFusedKAhead) % S, jj + kFusedKAhead, k_consumed);",
-         "dma(ks, (jj + kFusedKAhead + 2) % S, jj + kFusedKAhead + 2, k_consumed);"),
-        ("wait_allow(3);", "wait_allow(4);"),
-        ("wait_allow(0);                               // every", "wait_allow(3);                               // every"),
+        [("dma(ks, (jj + kFusedKAhead) % S, jj + kFusedKAhead, k_consumed);",
+          "dma(ks, (jj + kFusedKAhead + 2) % S, jj + kFusedKAhead + 2, k_consumed);")],
+        [("for (int x = 0; x < S - 1; ++x) dma(vs, x, x, -1);", "for (int x = 0; x < S; ++x) dma(vs, x, x, -1);"),
+         ("dma(vs, (jj + kFusedVAhead) % S, jj + kFusedVAhead, v_consumed);",
+          "dma(vs, (jj + kFusedVAhead + 1) % S, jj + kFusedVAhead + 1, v_consumed);")],
+        [("wait_allow(3);", "wait_allow(4);")],
+        [("wait_allow(0);                               // every", "wait_allow(3);                               // every")],
     ]
-    for i, (old, new) in enumerate(plants):
-        assert old in PROGRAM
+    for i, subs in enumerate(plants):
+        prog = PROGRAM
+        for old, new in subs:
+            assert old in prog
+            prog = prog.replace(old, new)
         src = tmp_path / f"sched_bad{i}.cpp"
-        src.write_text(PROGRAM.replace(old, new))
+        src.write_text(prog)
         exe = tmp_path / f"sched_bad{i}"
         r = subprocess.run(["g++", "-std=c++17", "-O1", f"-I{CSRC}", str(src), "-o", str(exe)], capture_output=True,
                            text=True)

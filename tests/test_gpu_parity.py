@@ -121,6 +121,40 @@ def test_causal_work_layouts(fa, oracle_mod):
             check(oracle_mod, run_bits(fa, kernel, q, k, v, True), ref, f"causal layout {kernel} {(B, H, N, D)}")
 
 
+def growing_logit_inputs(oracle_mod, B, H, N, D, seed):
+    """Q ~ 0.5 + noise, K rows growing linearly along the sequence: every
+    query's logits rise key after key, to about +60 at the last key, so the
+    running max moves on (nearly) every 32-key tile and the fused kernels take
+    their base-move path over and over. `reverse` of the same data (largest
+    key first) never moves it."""
+    rng = np.random.default_rng(seed)
+    kappa = 120.0 / np.sqrt(D)  # scale * D * 0.5 * kappa = 60 at the last key
+    ramp = kappa * np.arange(N, dtype=np.float64) / N
+    q = 0.5 + 0.05 * rng.standard_normal((B, H, N, D))
+    k = ramp[None, None, :, None] + 0.25 * rng.standard_normal((B, H, N, D))
+    v = rng.uniform(-1.0, 1.0, (B, H, N, D))
+    return (oracle_mod.bf16_bits(q), oracle_mod.bf16_bits(k), oracle_mod.bf16_bits(v))
+
+
+def test_base_moves(fa, oracle_mod):
+    """Inputs whose row max keeps growing (the exponent base moves on most
+    tiles), the same keys in falling order (it never moves after the first
+    tile), and N(0, 3^2) logits at a short length: all against the oracle,
+    dense and causal, both fused configurations, both head dims."""
+    for D in (64, 128):
+        for N in (256, 1000):
+            q, k, v = growing_logit_inputs(oracle_mod, 1, 2, N, D, seed=N + D)
+            cases = [("growing", q, k, v), ("falling", q, k[:, :, ::-1].copy(), v[:, :, ::-1].copy())]
+            cases.append(("stress",) + tuple(oracle_mod.make_inputs(1, 2, N, D, "stress")))
+            for name, qq, kk, vv in cases:
+                for causal in (False, True):
+                    ref = oracle_mod.attention(qq, kk, vv, causal, threads=HOST_THREADS)
+                    for kernel in ("v3_mfma", "v3b_mfma"):
+                        say("base moves", name, kernel, N, D, causal)
+                        check(oracle_mod, run_bits(fa, kernel, qq, kk, vv, causal), ref,
+                              f"base moves {name} {kernel} {(N, D, causal)}")
+
+
 def test_v3_and_v3b_agree(fa, oracle_mod):
     """Dense: each wave computes its 32 rows identically whatever the workgroup
     size (both configurations split the same KV range the same way), so the
