@@ -31,7 +31,8 @@ FA_ERROR_UNSUPPORTED = 801
 KERNEL_UNFUSED = 0
 KERNEL_V3 = 1
 KERNEL_V3B = 2
-KERNEL_IDS = {"v0_unfused": KERNEL_UNFUSED, "v3_mfma": KERNEL_V3, "v3b_mfma": KERNEL_V3B}
+KERNEL_V3_128 = 3  # the fused forward pinned to 128 rows per workgroup
+KERNEL_IDS = {"v0_unfused": KERNEL_UNFUSED, "v3_mfma": KERNEL_V3, "v3b_mfma": KERNEL_V3B, "v3_128": KERNEL_V3_128}
 
 _lib = None
 
@@ -81,6 +82,7 @@ _SIGNATURES = {
     "fa_launch_attention_unfused_profile": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp, _vp]),
     "fa_tensorcore_v3_supported": (_i, [_i]),
     "fa_launch_attention_tensorcore_v3": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp]),
+    "fa_launch_attention_fused": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp]),
     "fa_query_tensorcore_v3": (_i, [_i, ctypes.POINTER(TilingInfo)]),
     "fa_tensorcore_v3_hbm_bytes": (ctypes.c_double, [_i, _i, _i, _i, _i]),
     "fa_tensorcore_v3b_supported": (_i, [_i]),
@@ -240,11 +242,21 @@ def launch_attention_unfused_profile(q, k, v, o, workspace, shape, causal: bool,
 
 
 def launch_attention_tensorcore_v3(q, k, v, o, shape, causal: bool, stream=None) -> bool:
-    """include/flash_attention.h:92 — the fused MFMA forward (128 query rows / workgroup)."""
+    """include/flash_attention.h:92 — the fused MFMA forward (128 query rows / workgroup;
+    64 when the 128-row grid has fewer workgroups than the device has CUs)."""
     s = _shape_of(shape)
     st = lib().fa_launch_attention_tensorcore_v3(_ptr(q), _ptr(k), _ptr(v), _ptr(o), s.batch, s.heads,
                                                  s.seq_len, s.head_dim, int(causal), _stream(stream))
     return _check(st, "fa_launch_attention_tensorcore_v3")
+
+
+def launch_attention_fused(q, k, v, o, shape, causal: bool, rows_per_block: int = 0, stream=None) -> bool:
+    """The fused forward with a pinned workgroup configuration (no counterpart in
+    the reference): rows_per_block 128 (v3), 64 (v3b) or 0 (the v3 entry's choice)."""
+    s = _shape_of(shape)
+    st = lib().fa_launch_attention_fused(_ptr(q), _ptr(k), _ptr(v), _ptr(o), s.batch, s.heads, s.seq_len,
+                                         s.head_dim, int(causal), int(rows_per_block), _stream(stream))
+    return _check(st, "fa_launch_attention_fused")
 
 
 def launch_attention_tensorcore_v3b(q, k, v, o, shape, causal: bool, stream=None) -> bool:
@@ -320,6 +332,9 @@ def attention_forward(q, k, v, causal: bool = False, kernel: str = "v3_mfma", ou
             raise ValueError(f"head_dim {shape.head_dim} is not supported by the fused kernel")
     elif kernel == "v3b_mfma":
         if not launch_attention_tensorcore_v3b(q, k, v, o, shape, causal):
+            raise ValueError(f"head_dim {shape.head_dim} is not supported by the fused kernel")
+    elif kernel == "v3_128":
+        if not launch_attention_fused(q, k, v, o, shape, causal, rows_per_block=128):
             raise ValueError(f"head_dim {shape.head_dim} is not supported by the fused kernel")
     else:
         raise ValueError(f"unknown kernel {kernel!r}")

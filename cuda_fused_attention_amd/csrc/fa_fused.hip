@@ -946,6 +946,18 @@ int launch_fused(const void* q, const void* k, const void* v, void* o, int batch
     return static_cast<int>(hipGetLastError());
 }
 
+// Rows per workgroup the v3 entry point uses for a shape: 128, unless the
+// 128-row grid leaves compute units idle (fewer workgroups than CUs, small
+// batch*heads*seq_len), where the 64-row configuration's twice as many
+// workgroups finish sooner. Dense outputs are bitwise identical either way
+// (each wave computes its 32 rows the same way in both).
+int auto_rows_per_block(int batch, int heads, int seq_len)
+{
+    if (batch <= 0 || heads <= 0 || seq_len <= 0) return 128;
+    const long long wgs = static_cast<long long>(batch) * heads * ((static_cast<long long>(seq_len) + 127) / 128);
+    return wgs < device_compute_units() ? 64 : 128;
+}
+
 template <int kWpg>
 int query_fused(int head_dim, fa_tiling_info* info)
 {
@@ -1015,10 +1027,19 @@ extern "C" {
 
 int fa_tensorcore_v3_supported(int head_dim) { return head_dim == 64 || head_dim == 128; }
 
+int fa_launch_attention_fused(const void* q, const void* k, const void* v, void* o, int batch, int heads,
+                              int seq_len, int head_dim, int causal, int rows_per_block, void* stream)
+{
+    if (rows_per_block == 0) rows_per_block = auto_rows_per_block(batch, heads, seq_len);
+    if (rows_per_block == 128) return launch_fused<4>(q, k, v, o, batch, heads, seq_len, head_dim, causal, stream);
+    if (rows_per_block == 64) return launch_fused<2>(q, k, v, o, batch, heads, seq_len, head_dim, causal, stream);
+    return hipErrorInvalidValue;
+}
+
 int fa_launch_attention_tensorcore_v3(const void* q, const void* k, const void* v, void* o, int batch, int heads,
                                       int seq_len, int head_dim, int causal, void* stream)
 {
-    return launch_fused<4>(q, k, v, o, batch, heads, seq_len, head_dim, causal, stream);
+    return fa_launch_attention_fused(q, k, v, o, batch, heads, seq_len, head_dim, causal, 0, stream);
 }
 
 int fa_query_tensorcore_v3(int head_dim, fa_tiling_info* info) { return query_fused<4>(head_dim, info); }

@@ -94,10 +94,21 @@ int fa_tensorcore_v3_supported(int head_dim);
 /* include/flash_attention.h:92, kernels/v3/v3_tensorcore.cu:722-750 — the
  * fused forward: QK^T and PV on gfx950 bf16 MFMA (v_mfma_f32_32x32x16_bf16),
  * K and V^T staged in LDS, online softmax in fp32 registers, whole KV tiles
- * above the causal diagonal skipped. */
+ * above the causal diagonal skipped. 128 query rows per workgroup; a shape
+ * whose 128-row grid has fewer workgroups than the device has CUs runs the
+ * 64-row configuration instead (fa_launch_attention_fused, rows 0). */
 int fa_launch_attention_tensorcore_v3(const void* q, const void* k, const void* v, void* o,
                                       int batch, int heads, int seq_len, int head_dim,
                                       int causal, void* stream);
+
+/* No counterpart in the reference (whose v3 has one tile configuration): the
+ * fused forward with an explicit workgroup configuration. rows_per_block is
+ * 128 (the v3 configuration), 64 (the v3b configuration) or 0 (the choice
+ * fa_launch_attention_tensorcore_v3 makes); anything else returns
+ * hipErrorInvalidValue. For callers and tests that pin the configuration. */
+int fa_launch_attention_fused(const void* q, const void* k, const void* v, void* o,
+                              int batch, int heads, int seq_len, int head_dim,
+                              int causal, int rows_per_block, void* stream);
 
 /* include/flash_attention.h:94, kernels/v3/v3_tensorcore.cu:752-790 */
 int fa_query_tensorcore_v3(int head_dim, fa_tiling_info* info);
@@ -120,7 +131,8 @@ double fa_tensorcore_v3b_hbm_bytes(int batch, int heads, int seq_len, int head_d
 
 /* Harness support (benchmarks/bench_flash_attention.cu:265-299): run
  * `warmup` untimed launches of kernel `which` (0 = unfused, 1 = v3 fused,
- * 2 = v3b fused), synchronise, then `iters` launches each bracketed by
+ * 2 = v3b fused, 3 = fused with 128 rows per workgroup whatever the shape),
+ * synchronise, then `iters` launches each bracketed by
  * hipEventRecord on `stream`; elapsed milliseconds go to samples_ms[iters].
  * Returns FA_ERROR_UNSUPPORTED for an unsupported head_dim and
  * hipErrorInvalidValue for a non-positive or non-finite sample. */

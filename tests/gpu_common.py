@@ -48,6 +48,8 @@ def run(fa, kernel: str, q, k, v, causal: bool, stream=None, out=None):
         assert fa.launch_attention_tensorcore_v3(q, k, v, o, shape, causal, stream=st)
     elif kernel == "v3b_mfma":
         assert fa.launch_attention_tensorcore_v3b(q, k, v, o, shape, causal, stream=st)
+    elif kernel == "v3_128":
+        assert fa.launch_attention_fused(q, k, v, o, shape, causal, rows_per_block=128, stream=st)
     else:
         raise ValueError(kernel)
     torch.cuda.synchronize()
@@ -59,4 +61,7 @@ def run_bits(fa, kernel, qb, kb, vb, causal):
     return from_dev(run(fa, kernel, q, k, v, causal))
 
 
-KERNELS = ["v0_unfused", "v3_mfma", "v3b_mfma"]
+# v3_mfma picks its workgroup configuration from the shape (64 rows for
+# grids that leave CUs idle); v3_128 pins the 128-row one, so small shapes
+# still exercise it.
+KERNELS = ["v0_unfused", "v3_mfma", "v3b_mfma", "v3_128"]

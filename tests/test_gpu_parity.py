@@ -116,7 +116,7 @@ def test_causal_work_layouts(fa, oracle_mod):
     for (B, H, N, D) in cases:
         q, k, v = oracle_mod.make_inputs(B, H, N, D, seeds={"q": 41, "k": 42, "v": 43})
         ref = oracle_mod.attention(q, k, v, True, threads=HOST_THREADS)
-        for kernel in ("v3_mfma", "v3b_mfma"):
+        for kernel in ("v3_mfma", "v3b_mfma", "v3_128"):
             say("causal layout", kernel, B, H, N, D)
             check(oracle_mod, run_bits(fa, kernel, q, k, v, True), ref, f"causal layout {kernel} {(B, H, N, D)}")
 
@@ -149,26 +149,26 @@ def test_base_moves(fa, oracle_mod):
             for name, qq, kk, vv in cases:
                 for causal in (False, True):
                     ref = oracle_mod.attention(qq, kk, vv, causal, threads=HOST_THREADS)
-                    for kernel in ("v3_mfma", "v3b_mfma"):
+                    for kernel in ("v3_mfma", "v3b_mfma", "v3_128"):
                         say("base moves", name, kernel, N, D, causal)
                         check(oracle_mod, run_bits(fa, kernel, qq, kk, vv, causal), ref,
                               f"base moves {name} {kernel} {(N, D, causal)}")
 
 
 def test_v3_and_v3b_agree(fa, oracle_mod):
-    """Dense: each wave computes its 32 rows identically whatever the workgroup
-    size (both configurations split the same KV range the same way), so the
-    outputs are bitwise equal. Causal: the KV range a workgroup walks ends at
-    its own last row, so the 128-row and 64-row configurations split it
-    between their two wave groups at different tiles and sum in a different
-    order; both must pass the oracle gate and agree to one bf16 ulp of the
-    row scale."""
+    """The 128-row (v3_128) and 64-row (v3b) configurations. Dense: each wave
+    computes its 32 rows identically whatever the workgroup size (both
+    configurations split the same KV range the same way), so the outputs are
+    bitwise equal. Causal: the KV range a workgroup walks ends at its own last
+    row, so the two configurations split it between their two wave groups at
+    different tiles and sum in a different order; both must pass the oracle
+    gate and agree to one bf16 ulp of the row scale."""
     for (B, H, N, D) in [(1, 2, 300, 64), (2, 2, 513, 128)]:
         qb, kb, vb = oracle_mod.make_inputs(B, H, N, D)
         q, k, v = to_dev(qb), to_dev(kb), to_dev(vb)
         for causal in (False, True):
             say("v3-v3b", B, H, N, D, causal)
-            a = from_dev(run(fa, "v3_mfma", q, k, v, causal))
+            a = from_dev(run(fa, "v3_128", q, k, v, causal))
             b = from_dev(run(fa, "v3b_mfma", q, k, v, causal))
             if not causal:
                 assert np.array_equal(a, b)
@@ -180,6 +180,24 @@ def test_v3_and_v3b_agree(fa, oracle_mod):
             bf = oracle_mod.bf16_to_f32(b).astype(np.float64).reshape(-1, D)
             row_scale = np.abs(ref.reshape(-1, D)).max(axis=1, keepdims=True)
             assert np.all(np.abs(af - bf) <= 2.0 ** -7 * row_scale)
+
+
+def test_v3_picks_the_configuration_by_grid(fa, oracle_mod):
+    """The v3 entry runs 64 rows per workgroup when the 128-row grid has fewer
+    workgroups than the device has CUs, else 128: its output equals the
+    pinned configuration's bit for bit (dense and causal), on each side of
+    the threshold."""
+    cus = fa.query_tensorcore_v3(64)["compute_units"]
+    assert cus > 0
+    below = (1, 2, 700, 64)                       # 2 * 6 = 12 workgroups of 128 rows
+    at = (1, cus // 2, 256, 64)                   # exactly `cus` workgroups of 128 rows
+    for (B, H, N, D), pinned in ((below, "v3b_mfma"), (at, "v3_128")):
+        q, k, v = (to_dev(x) for x in oracle_mod.make_inputs(B, H, N, D))
+        for causal in (False, True):
+            say("v3 dispatch", B, H, N, D, causal, pinned)
+            a = from_dev(run(fa, "v3_mfma", q, k, v, causal))
+            b = from_dev(run(fa, pinned, q, k, v, causal))
+            assert np.array_equal(a, b), (B, H, N, D, causal, pinned)
 
 
 def test_deterministic(fa, oracle_mod):
