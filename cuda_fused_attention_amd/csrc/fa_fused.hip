@@ -223,11 +223,19 @@ __device__ __forceinline__ void dma_lane_offsets(int wg, int lane, uint32_t (&vo
 
 // Buffer resource of the K or V tile starting at key kv0 (< n): it ends at
 // the slab's last row, so rows of a tail tile past the sequence end read as
-// zero (finite; their scores are masked).
+// zero (finite; their scores are masked). Built with a plain 64-bit add
+// (s_add_u32 + s_addc_u32): every copy recomputes it, so its scalar
+// instruction count is part of every step.
 template <int D>
 __device__ __forceinline__ i32x4 tile_rsrc(ScalarPtr slab, int kv0, int n)
 {
-    return make_rsrc(slab, static_cast<uint32_t>(kv0 * (D * 2)), static_cast<uint32_t>((n - kv0) * (D * 2)));
+    const uint64_t base = ((static_cast<uint64_t>(slab.hi) << 32) | slab.lo) + static_cast<uint32_t>(kv0 * (D * 2));
+    i32x4 r;
+    r[0] = static_cast<int>(static_cast<uint32_t>(base));
+    r[1] = static_cast<int>(static_cast<uint32_t>(base >> 32));  // < 2^16 (48-bit addresses): stride 0
+    r[2] = (n - kv0) * (D * 2);
+    r[3] = static_cast<int>(kRawBufferConfig);
+    return r;
 }
 
 // Copy u of this wave's share of one K or V tile.
@@ -502,6 +510,10 @@ __global__ __launch_bounds__(128 * kWpg) void fused_attention_kernel(const uint1
         const int tb = G == 0 ? 0 : split.first1;                 // first tile of this group
         const int cnt = G == 0 ? split.count0 : split.count1;
         const int lw = min(cnt - 1, t_last - tb);                 // last local tile this wave computes
+        // First step whose "next" tile needs the per-element mask: the
+        // diagonal / tail tile, or the dummy product after the wave's last
+        // tile (steps run jj <= lw).
+        const int j_mask = min(lw, t_mask - tb - 1);
 
         // DMA lane offsets (full tiles and the tail tile) and copy helpers.
         // Every copy point issues a fixed number of copies so the vmcnt
@@ -714,9 +726,8 @@ __global__ __launch_bounds__(128 * kWpg) void fused_attention_kernel(const uint1
             // exponentials. On the wave's last tile (jj == lw) the "next" S^T
             // is a dummy product with a landed stage: masking all of it makes
             // its P and sums zero.
-            const int t_next = tb + jj + 1;
-            if (t_next >= t_mask || jj == lw)
-                mask_tile(sbuf[B ^ 1], jj == lw ? -kTileKV : dead_base - t_next * kTileKV);
+            if (jj >= j_mask)
+                mask_tile(sbuf[B ^ 1], jj == lw ? -kTileKV : dead_base - (tb + jj + 1) * kTileKV);
             __builtin_amdgcn_sched_barrier(0);
             const bf16x8 p_cur[2] = {p_lo[B], p_hi};
             tsum = 0.0f;
