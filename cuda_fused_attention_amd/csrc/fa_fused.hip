@@ -711,6 +711,12 @@ __global__ __launch_bounds__(128 * kWpg) void fused_attention_kernel(const uint1
         auto block_b = [&](auto par_tag, int jj) {
             constexpr int P = decltype(par_tag)::value;
             constexpr int B = P & 1;
+            // Head dim 128, dense: the wave of group 1 takes issue priority
+            // over its SIMD partner for this block. The SIMD otherwise
+            // favours the older group-0 wave, which then idles at the next
+            // barrier while group 1 finishes (measured 1% per launch).
+            constexpr bool kLeadB = G == 1 && D == 128 && !kCausal;
+            if constexpr (kLeadB) __builtin_amdgcn_s_setprio(1);
             const bool rare = __any(tsum > kSumLimit);
             if (rare)
             {
@@ -746,6 +752,7 @@ __global__ __launch_bounds__(128 * kWpg) void fused_attention_kernel(const uint1
             pin(tsum);
             if (rare) rebase(par_tag, jj);
             pin(rs.l);
+            if constexpr (kLeadB) __builtin_amdgcn_s_setprio(0);
         };
 
         // Steps this wave computes (tiles up to its diagonal / the group's
