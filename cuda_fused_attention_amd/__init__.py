@@ -32,7 +32,9 @@ KERNEL_UNFUSED = 0
 KERNEL_V3 = 1
 KERNEL_V3B = 2
 KERNEL_V3_128 = 3  # the fused forward pinned to 128 rows per workgroup
-KERNEL_IDS = {"v0_unfused": KERNEL_UNFUSED, "v3_mfma": KERNEL_V3, "v3b_mfma": KERNEL_V3B, "v3_128": KERNEL_V3_128}
+KERNEL_V3_256 = 4  # pinned to 256 rows per workgroup (one wave group; head_dim 128)
+KERNEL_IDS = {"v0_unfused": KERNEL_UNFUSED, "v3_mfma": KERNEL_V3, "v3b_mfma": KERNEL_V3B, "v3_128": KERNEL_V3_128,
+              "v3_256": KERNEL_V3_256}
 
 _lib = None
 
@@ -83,6 +85,7 @@ _SIGNATURES = {
     "fa_tensorcore_v3_supported": (_i, [_i]),
     "fa_launch_attention_tensorcore_v3": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp]),
     "fa_launch_attention_fused": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp]),
+    "fa_query_fused": (_i, [_i, _i, ctypes.POINTER(TilingInfo)]),
     "fa_query_tensorcore_v3": (_i, [_i, ctypes.POINTER(TilingInfo)]),
     "fa_tensorcore_v3_hbm_bytes": (ctypes.c_double, [_i, _i, _i, _i, _i]),
     "fa_tensorcore_v3b_supported": (_i, [_i]),
@@ -184,6 +187,12 @@ def query_tensorcore_v3(head_dim: int) -> dict:
     return info.as_dict()
 
 
+def query_fused(head_dim: int, rows_per_block: int) -> dict:
+    info = TilingInfo()
+    _check(lib().fa_query_fused(head_dim, rows_per_block, ctypes.byref(info)), "fa_query_fused")
+    return info.as_dict()
+
+
 def query_tensorcore_v3b(head_dim: int) -> dict:
     info = TilingInfo()
     _check(lib().fa_query_tensorcore_v3b(head_dim, ctypes.byref(info)), "fa_query_tensorcore_v3b")
@@ -252,7 +261,8 @@ def launch_attention_tensorcore_v3(q, k, v, o, shape, causal: bool, stream=None)
 
 def launch_attention_fused(q, k, v, o, shape, causal: bool, rows_per_block: int = 0, stream=None) -> bool:
     """The fused forward with a pinned workgroup configuration (no counterpart in
-    the reference): rows_per_block 128 (v3), 64 (v3b) or 0 (the v3 entry's choice)."""
+    the reference): rows_per_block 128 (v3), 64 (v3b), 256 (one wave group, head_dim
+    128) or 0 (the v3 entry's choice)."""
     s = _shape_of(shape)
     st = lib().fa_launch_attention_fused(_ptr(q), _ptr(k), _ptr(v), _ptr(o), s.batch, s.heads, s.seq_len,
                                          s.head_dim, int(causal), int(rows_per_block), _stream(stream))
@@ -333,8 +343,8 @@ def attention_forward(q, k, v, causal: bool = False, kernel: str = "v3_mfma", ou
     elif kernel == "v3b_mfma":
         if not launch_attention_tensorcore_v3b(q, k, v, o, shape, causal):
             raise ValueError(f"head_dim {shape.head_dim} is not supported by the fused kernel")
-    elif kernel == "v3_128":
-        if not launch_attention_fused(q, k, v, o, shape, causal, rows_per_block=128):
+    elif kernel in ("v3_128", "v3_256"):
+        if not launch_attention_fused(q, k, v, o, shape, causal, rows_per_block=int(kernel[3:])):
             raise ValueError(f"head_dim {shape.head_dim} is not supported by the fused kernel")
     else:
         raise ValueError(f"unknown kernel {kernel!r}")

@@ -91,24 +91,35 @@ constexpr int kTileKV = fa::kFusedTileKV;  // keys per LDS tile
 constexpr int kStages = fa::kFusedStages;  // LDS stages per tensor per group
 constexpr float kSumLimit = 256.0f;        // a tile's partial row sum above this moves the exponent base
 
+// How the kWpg waves of one group share the copies of a K or V tile.
 template <int D, int kWpg>
-struct Cfg
+struct TileCopy
 {
-    static constexpr int kRows = 32 * kWpg;                            // query rows per workgroup
-    static constexpr int kThreads = 128 * kWpg;                        // two groups of kWpg waves
     static constexpr int kChunks = D / 8;                              // 16-byte chunks per row
-    static constexpr int kTileElems = kTileKV * D;                     // bf16 per K or V tile
     static constexpr int kRowsPerIssue = 64 / kChunks;                 // rows one 64-lane DMA covers
     static constexpr int kIssues = kTileKV / (kRowsPerIssue * kWpg);   // DMA issues per wave per tile
+    static_assert(kIssues >= 1 && kIssues * kRowsPerIssue * kWpg == kTileKV, "tile splits evenly over a group");
+};
+
+// kGroups wave groups of kWpg waves (one wave per 32-row slot in each
+// group): 2 splits the KV range between the groups (split-KV inside the
+// workgroup), 1 walks it whole with every wave on one tile stream.
+template <int D, int kWpg, int kGroups = 2>
+struct Cfg : TileCopy<D, kWpg>
+{
+    using TileCopy<D, kWpg>::kIssues;
+    static constexpr int kRows = 32 * kWpg;                            // query rows per workgroup
+    static constexpr int kThreads = 64 * kGroups * kWpg;
+    static constexpr int kTileElems = kTileKV * D;                     // bf16 per K or V tile
     static constexpr int kGroupElems = 2 * kStages * kTileElems;       // one group's K and V stages
-    static constexpr int kLdsElems = 2 * kGroupElems;
+    static constexpr int kLdsElems = kGroups * kGroupElems;
     static constexpr int kQElems = kWpg * 32 * D;                      // Q rows of the kWpg slots
     static constexpr int kQIssues = 32 * D * 2 / 1024;                 // DMA issues per slot's Q rows
-    static constexpr int kQIssuesPerWave = kWpg * kQIssues / (2 * kWpg);
+    static constexpr int kQIssuesPerWave = kQIssues / kGroups;
     static_assert(D == 64 || D == 128, "head_dim 64 or 128");
-    static_assert(kIssues * kRowsPerIssue * kWpg == kTileKV, "tile splits evenly over a group");
+    static_assert(kGroups == 1 || kGroups == 2, "one or two wave groups");
     static_assert(2 * kIssues < 64, "vmcnt range");
-    static_assert(kQIssuesPerWave * 2 * kWpg == kWpg * kQIssues, "Q copies split evenly over the waves");
+    static_assert(kQIssuesPerWave * kGroups == kQIssues, "Q copies split evenly over the waves");
     static_assert((kLdsElems + kQElems) * 2 <= 160 * 1024, "LDS of one workgroup");
 };
 
@@ -207,9 +218,9 @@ __device__ __forceinline__ uint32_t lds_addr(const uint16_t* p)
 // chosen so that the chunk lands at its swizzled position (the copy writes
 // lane l's 16 bytes to LDS byte 16*l of the copy's 1 KiB block).
 template <int D, int kWpg, bool kIsV>
-__device__ __forceinline__ void dma_lane_offsets(int wg, int lane, uint32_t (&voff)[Cfg<D, kWpg>::kIssues])
+__device__ __forceinline__ void dma_lane_offsets(int wg, int lane, uint32_t (&voff)[TileCopy<D, kWpg>::kIssues])
 {
-    using C = Cfg<D, kWpg>;
+    using C = TileCopy<D, kWpg>;
     const int sub_row = lane / C::kChunks;
     const int pchunk = lane % C::kChunks;
 #pragma unroll
@@ -241,7 +252,7 @@ __device__ __forceinline__ i32x4 tile_rsrc(ScalarPtr slab, int kv0, int n)
 // Copy u of this wave's share of one K or V tile.
 template <int D, int kWpg>
 __device__ __forceinline__ void dma_copy(i32x4 rsrc, uint32_t stage_lds, int wg_s, int u,
-                                         const uint32_t (&voff)[Cfg<D, kWpg>::kIssues])
+                                         const uint32_t (&voff)[TileCopy<D, kWpg>::kIssues])
 {
     dma16(rsrc, voff[u], stage_lds + (u * kWpg + wg_s) * 1024);
 }
@@ -408,15 +419,15 @@ __device__ __forceinline__ void rescale_o(Frag<D>& f, float alpha)
         for (int r = 0; r < 16; ++r) f.o[db][r] *= alpha;
 }
 
-template <int D, int kWpg, bool kCausal>
-__global__ __launch_bounds__(128 * kWpg) void fused_attention_kernel(const uint16_t* __restrict__ q,
-                                                                     const uint16_t* __restrict__ k,
-                                                                     const uint16_t* __restrict__ v,
-                                                                     uint16_t* __restrict__ o, int n,
-                                                                     int q_blocks, int total_blocks,
-                                                                     float c_log2, int paired)
+template <int D, int kWpg, bool kCausal, int kGroups>
+__global__ __launch_bounds__(64 * kGroups * kWpg) void fused_attention_kernel(const uint16_t* __restrict__ q,
+                                                                              const uint16_t* __restrict__ k,
+                                                                              const uint16_t* __restrict__ v,
+                                                                              uint16_t* __restrict__ o, int n,
+                                                                              int q_blocks, int total_blocks,
+                                                                              float c_log2, int paired)
 {
-    using C = Cfg<D, kWpg>;
+    using C = Cfg<D, kWpg, kGroups>;
     // Group g's K stages, then its V stages, at compile-time offsets of one
     // LDS array, so every operand read is a per-lane base plus an immediate;
     // the Q rows of the workgroup's slots follow.
@@ -426,7 +437,7 @@ __global__ __launch_bounds__(128 * kWpg) void fused_attention_kernel(const uint1
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const int grp = wave / kWpg;      // KV half
+    const int grp = kGroups == 1 ? 0 : wave / kWpg;  // KV half (always 0 with one group)
     const int wg = wave % kWpg;       // row block within the workgroup
     const int wg_s = __builtin_amdgcn_readfirstlane(wg);  // same value, in an SGPR
     const int i = lane & 31;
@@ -452,7 +463,7 @@ __global__ __launch_bounds__(128 * kWpg) void fused_attention_kernel(const uint1
     //   waves sharing a SIMD (w and w + kWpg) hold one early and one late
     //   half block.
     const int grp_s = __builtin_amdgcn_readfirstlane(grp);
-    const bool pair_rows = kCausal && paired != 0;
+    const bool pair_rows = kCausal && kGroups == 2 && paired != 0;
     const int slot = (pair_rows && grp_s == 1) ? (wg_s + kWpg / 2) % kWpg : wg_s;
     constexpr int kHalfRows = C::kRows / 2;
     const int n_half = (n + kHalfRows - 1) / kHalfRows;
@@ -479,7 +490,7 @@ __global__ __launch_bounds__(128 * kWpg) void fused_attention_kernel(const uint1
 
     const int last_key = kCausal ? min(last_row, n - 1) : n - 1;
     const int n_tiles = last_key / kTileKV + 1;
-    const fa::FusedSplit split = fa::fused_split(n_tiles);
+    const fa::FusedSplit split = kGroups == 2 ? fa::fused_split(n_tiles) : fa::fused_single(n_tiles);
 
     // Tiles from t_mask on need the per-element mask (sequence tail, or this
     // wave's diagonal); tiles after t_last lie wholly above the diagonal.
@@ -788,9 +799,62 @@ __global__ __launch_bounds__(128 * kWpg) void fused_attention_kernel(const uint1
         barrier();
     };
 
-    if (grp == 0) run_group(std::integral_constant<int, 0>{});
+    if constexpr (kGroups == 1) run_group(std::integral_constant<int, 0>{});
+    else if (grp == 0) run_group(std::integral_constant<int, 0>{});
     else run_group(std::integral_constant<int, 1>{});
 
+    // Normalise O^T blocks [kFirstDb, kFirstDb + kNumDb) of this wave's 32
+    // rows by `inv` and store them (head dims 32*kFirstDb ..): O^T (lane =
+    // query) is transposed through `obuf` (32 rows of 32*kNumDb bf16, only
+    // this wave touches it now) into row-major bf16 with XOR-swizzled 16-byte
+    // chunks, then stored as contiguous 16-byte pieces of the rows.
+    auto store_rows = [&](auto first_tag, auto num_tag, uint16_t* obuf, float inv) {
+        constexpr int kFirstDb = decltype(first_tag)::value;
+        constexpr int kNumDb = decltype(num_tag)::value;
+        constexpr int kCols = 32 * kNumDb;
+        constexpr int kColChunks = kCols / 8;
+#pragma unroll
+        for (int b = 0; b < kNumDb; ++b)
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+            {
+                uint2 packed;
+                packed.x = fa::pack_bf16x2(f.o[kFirstDb + b][4 * g + 0] * inv, f.o[kFirstDb + b][4 * g + 1] * inv);
+                packed.y = fa::pack_bf16x2(f.o[kFirstDb + b][4 * g + 2] * inv, f.o[kFirstDb + b][4 * g + 3] * inv);
+                const int chunk = (4 * b + g) ^ (i & (kColChunks - 1));
+                *reinterpret_cast<uint2*>(obuf + i * kCols + chunk * 8 + 4 * h) = packed;
+            }
+        wait_vm_lgkm0<63>();
+#pragma unroll
+        for (int u = 0; u < kColChunks / 2; ++u)
+        {
+            const int x = u * 64 + lane;
+            const int row = x / kColChunks;
+            const int c = x % kColChunks;
+            const uint4 chunk = *reinterpret_cast<const uint4*>(obuf + row * kCols + ((c ^ (row & (kColChunks - 1))) * 8));
+            if (wq0 + row < n)
+                *reinterpret_cast<uint4*>(o + slab_off + static_cast<size_t>(wq0 + row) * D + kFirstDb * 32 + c * 8) = chunk;
+        }
+    };
+
+    // The two lane halves hold partial row sums of the same query.
+    auto inv_row_sum = [&](float l) {
+        const float l_tot = l + __shfl_xor(l, 32, 64);
+        return l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+    };
+
+    if constexpr (kGroups == 1)
+    {
+        // One group: every wave holds its rows' whole O^T. All DMAs have
+        // landed (every wave drained its own before the last barrier), so
+        // the stage area is free: each wave transposes through its own 32
+        // rows of it.
+        static_assert(kWpg * 32 * D <= C::kLdsElems, "transpose staging fits the stage area");
+        store_rows(std::integral_constant<int, 0>{}, std::integral_constant<int, D / 32>{}, lds + slot * 32 * D,
+                   inv_row_sum(rs.l));
+    }
+    else
+    {
     // Merge and epilogue, split over both groups: the wave of group g
     // finalises head dims [g*D/2, (g+1)*D/2) of its slot's 32 rows. It sends
     // the other half of its O^T, its exponent base and its partial row sums
@@ -839,64 +903,42 @@ __global__ __launch_bounds__(128 * kWpg) void fused_attention_kernel(const uint1
 #pragma unroll
                 for (int j = 0; j < 4; ++j) f.o[kKeep + b][4 * r4 + j] = f.o[kKeep + b][4 * r4 + j] * a0 + x[j] * a1;
             }
-
-        // The two lane halves hold partial row sums of the same query. O^T
-        // (lane = query) is transposed through the received area (only this
-        // wave touches it now) into row-major bf16 with XOR-swizzled 16-byte
-        // chunks, then stored as contiguous 16-byte pieces of the rows.
-        const float l_tot = l + __shfl_xor(l, 32, 64);
-        const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-        constexpr int kHalfCols = D / 2;
-        constexpr int kHalfChunks = kHalfCols / 8;
-        uint16_t* const obuf = reinterpret_cast<uint16_t*>(x_recv);
+        const float inv = inv_row_sum(l);
         wait_vm_lgkm0<0>();  // received values are in registers before the area is reused
-#pragma unroll
-        for (int b = 0; b < kHalfDb; ++b)
-#pragma unroll
-            for (int g = 0; g < 4; ++g)
-            {
-                uint2 packed;
-                packed.x = fa::pack_bf16x2(f.o[kKeep + b][4 * g + 0] * inv, f.o[kKeep + b][4 * g + 1] * inv);
-                packed.y = fa::pack_bf16x2(f.o[kKeep + b][4 * g + 2] * inv, f.o[kKeep + b][4 * g + 3] * inv);
-                const int chunk = (4 * b + g) ^ (i & (kHalfChunks - 1));
-                *reinterpret_cast<uint2*>(obuf + i * kHalfCols + chunk * 8 + 4 * h) = packed;
-            }
-        wait_vm_lgkm0<63>();
-#pragma unroll
-        for (int u = 0; u < kHalfChunks / 2; ++u)
-        {
-            const int x = u * 64 + lane;
-            const int row = x / kHalfChunks;
-            const int c = x % kHalfChunks;
-            const uint4 chunk = *reinterpret_cast<const uint4*>(obuf + row * kHalfCols + ((c ^ (row & (kHalfChunks - 1))) * 8));
-            if (wq0 + row < n)
-                *reinterpret_cast<uint4*>(o + slab_off + static_cast<size_t>(wq0 + row) * D + G * kHalfCols + c * 8) = chunk;
-        }
+        store_rows(std::integral_constant<int, kKeep>{}, std::integral_constant<int, kHalfDb>{},
+                   reinterpret_cast<uint16_t*>(x_recv), inv);
     };
     if (grp_s == 0) finish(std::integral_constant<int, 0>{});
     else finish(std::integral_constant<int, 1>{});
+    }
 }
 
-template <int D, int kWpg, bool kCausal>
+template <int D, int kWpg, bool kCausal, int kGroups>
 const void* kernel_ptr()
 {
-    return reinterpret_cast<const void*>(&fused_attention_kernel<D, kWpg, kCausal>);
+    return reinterpret_cast<const void*>(&fused_attention_kernel<D, kWpg, kCausal, kGroups>);
 }
 
-template <int kWpg>
+template <int kWpg, int kGroups>
 const void* pick_kernel(int head_dim, bool causal)
 {
-    if (head_dim == 64) return causal ? kernel_ptr<64, kWpg, true>() : kernel_ptr<64, kWpg, false>();
-    if (head_dim == 128) return causal ? kernel_ptr<128, kWpg, true>() : kernel_ptr<128, kWpg, false>();
+    if (head_dim == 64)
+    {
+        if constexpr (kGroups == 1) return nullptr;  // a 4 KiB tile does not split over 8 waves' 1 KiB copies
+        else return causal ? kernel_ptr<64, kWpg, true, kGroups>() : kernel_ptr<64, kWpg, false, kGroups>();
+    }
+    if (head_dim == 128)
+        return causal ? kernel_ptr<128, kWpg, true, kGroups>() : kernel_ptr<128, kWpg, false, kGroups>();
     return nullptr;
 }
 
-template <int D, int kWpg, bool kCausal>
+template <int D, int kWpg, bool kCausal, int kGroups>
 void launch_typed(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o, int n, int q_blocks,
                   int total, float c_log2, int paired, hipStream_t stream)
 {
-    hipLaunchKernelGGL((fused_attention_kernel<D, kWpg, kCausal>), dim3(static_cast<unsigned>(total)),
-                       dim3(Cfg<D, kWpg>::kThreads), 0, stream, q, k, v, o, n, q_blocks, total, c_log2, paired);
+    hipLaunchKernelGGL((fused_attention_kernel<D, kWpg, kCausal, kGroups>), dim3(static_cast<unsigned>(total)),
+                       dim3(Cfg<D, kWpg, kGroups>::kThreads), 0, stream, q, k, v, o, n, q_blocks, total, c_log2,
+                       paired);
 }
 
 // Compute units of the current device (cached per device; 256 on an
@@ -916,11 +958,12 @@ int device_compute_units()
     return cus;
 }
 
-template <int kWpg>
+template <int kWpg, int kGroups = 2>
 int launch_fused(const void* q, const void* k, const void* v, void* o, int batch, int heads, int seq_len,
                  int head_dim, int causal, void* stream_ptr)
 {
     if (head_dim != 64 && head_dim != 128) return FA_ERROR_UNSUPPORTED;
+    if (kGroups == 1 && head_dim != 128) return hipErrorInvalidValue;
     if (batch < 0 || heads < 0 || seq_len < 0) return hipErrorInvalidValue;
     const long long bh = static_cast<long long>(batch) * heads;
     if (bh == 0 || seq_len == 0) return hipSuccess;
@@ -934,14 +977,15 @@ int launch_fused(const void* q, const void* k, const void* v, void* o, int batch
     // Workgroups per slab: one per 32*kWpg rows; causal grids that fit in
     // one round on the device instead get one per pair of 16*kWpg-row half
     // blocks (p, last - p), which evens out the triangle's work per
-    // workgroup. Larger causal grids keep whole blocks, issued heaviest
-    // first, and the dispatcher balances the rounds.
+    // workgroup (two-group configurations). Larger causal grids keep whole
+    // blocks, issued heaviest first, and the dispatcher balances the rounds.
     constexpr int rows = 32 * kWpg;
+    constexpr int threads = 64 * kGroups * kWpg;
     const long long blocks = (static_cast<long long>(seq_len) + rows - 1) / rows;
-    const int paired = (causal && bh * blocks <= device_compute_units()) ? 1 : 0;
+    const int paired = (kGroups == 2 && causal && bh * blocks <= device_compute_units()) ? 1 : 0;
     const long long q_blocks = paired ? ((static_cast<long long>(seq_len) + rows / 2 - 1) / (rows / 2) + 1) / 2 : blocks;
     const long long total = bh * q_blocks;
-    if (total > 0x7fffffffLL / (128 * kWpg)) return hipErrorInvalidValue;
+    if (total > 0x7fffffffLL / threads) return hipErrorInvalidValue;
 
     const float c_log2 = fa_default_scale(head_dim) * fa::kLog2e;
     hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
@@ -953,42 +997,56 @@ int launch_fused(const void* q, const void* k, const void* v, void* o, int batch
     const int tot = static_cast<int>(total);
     if (head_dim == 64)
     {
-        if (causal) launch_typed<64, kWpg, true>(qb, kb, vb, ob, seq_len, qbk, tot, c_log2, paired, stream);
-        else launch_typed<64, kWpg, false>(qb, kb, vb, ob, seq_len, qbk, tot, c_log2, 0, stream);
+        if constexpr (kGroups == 2)
+        {
+            if (causal) launch_typed<64, kWpg, true, kGroups>(qb, kb, vb, ob, seq_len, qbk, tot, c_log2, paired, stream);
+            else launch_typed<64, kWpg, false, kGroups>(qb, kb, vb, ob, seq_len, qbk, tot, c_log2, 0, stream);
+        }
     }
     else
     {
-        if (causal) launch_typed<128, kWpg, true>(qb, kb, vb, ob, seq_len, qbk, tot, c_log2, paired, stream);
-        else launch_typed<128, kWpg, false>(qb, kb, vb, ob, seq_len, qbk, tot, c_log2, 0, stream);
+        if (causal) launch_typed<128, kWpg, true, kGroups>(qb, kb, vb, ob, seq_len, qbk, tot, c_log2, paired, stream);
+        else launch_typed<128, kWpg, false, kGroups>(qb, kb, vb, ob, seq_len, qbk, tot, c_log2, 0, stream);
     }
     return static_cast<int>(hipGetLastError());
 }
 
-// Rows per workgroup the v3 entry point uses for a shape: 128, unless the
-// 128-row grid leaves compute units idle (fewer workgroups than CUs, small
-// batch*heads*seq_len), where the 64-row configuration's twice as many
-// workgroups finish sooner. Dense outputs are bitwise identical either way
+// Rows per workgroup the v3 entry point uses for a shape (measured on
+// MI355X):
+//   * 64 when the 128-row grid has fewer workgroups than CUs (small
+//     batch*heads*seq_len): twice as many workgroups finish sooner;
+//   * 256 (one wave group, head_dim 128) when even 256-row workgroups give
+//     every CU one (dense), or, causal, for seq_len >= 8192 with at least two
+//     rounds of them: half the L2->LDS copies per score and no merge, 4-7%
+//     faster there; shorter causal sequences lose more to the coarser
+//     diagonal blocks than they gain;
+//   * 128 otherwise.
+// Dense outputs of the 64- and 128-row configurations are bitwise identical
 // (each wave computes its 32 rows the same way in both).
-int auto_rows_per_block(int batch, int heads, int seq_len)
+int auto_rows_per_block(int batch, int heads, int seq_len, int head_dim, int causal)
 {
     if (batch <= 0 || heads <= 0 || seq_len <= 0) return 128;
-    const long long wgs = static_cast<long long>(batch) * heads * ((static_cast<long long>(seq_len) + 127) / 128);
-    return wgs < device_compute_units() ? 64 : 128;
+    const long long bh = static_cast<long long>(batch) * heads;
+    const long long cus = device_compute_units();
+    if (bh * ((static_cast<long long>(seq_len) + 127) / 128) < cus) return 64;
+    const long long wide = bh * ((static_cast<long long>(seq_len) + 255) / 256);
+    if (head_dim == 128 && (causal ? (seq_len >= 8192 && wide >= 2 * cus) : wide >= cus)) return 256;
+    return 128;
 }
 
-template <int kWpg>
+template <int kWpg, int kGroups = 2>
 int query_fused(int head_dim, fa_tiling_info* info)
 {
     if (!info) return hipErrorInvalidValue;
     *info = fa_tiling_info{};
-    if (head_dim != 64 && head_dim != 128) return hipSuccess;  // supported = 0
+    const void* func = pick_kernel<kWpg, kGroups>(head_dim, false);
+    if (!func) return hipSuccess;  // supported = 0
     info->supported = 1;
-    info->block_size = 128 * kWpg;
-    info->waves_per_block = 2 * kWpg;
+    info->block_size = 64 * kGroups * kWpg;
+    info->waves_per_block = kGroups * kWpg;
     info->tile_kv = kTileKV;
     info->rows_per_block = 32 * kWpg;
 
-    const void* func = pick_kernel<kWpg>(head_dim, false);
     hipFuncAttributes attr{};
     hipError_t e = hipFuncGetAttributes(&attr, func);
     if (e != hipSuccess) return e;
@@ -997,7 +1055,7 @@ int query_fused(int head_dim, fa_tiling_info* info)
     info->local_bytes_per_thread = static_cast<int>(attr.localSizeBytes);
 
     int blocks = 0;
-    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, func, 128 * kWpg, 0);
+    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, func, info->block_size, 0);
     if (e != hipSuccess) return e;
     info->max_blocks_per_sm = blocks;
 
@@ -1048,9 +1106,11 @@ int fa_tensorcore_v3_supported(int head_dim) { return head_dim == 64 || head_dim
 int fa_launch_attention_fused(const void* q, const void* k, const void* v, void* o, int batch, int heads,
                               int seq_len, int head_dim, int causal, int rows_per_block, void* stream)
 {
-    if (rows_per_block == 0) rows_per_block = auto_rows_per_block(batch, heads, seq_len);
+    if (rows_per_block == 0) rows_per_block = auto_rows_per_block(batch, heads, seq_len, head_dim, causal);
     if (rows_per_block == 128) return launch_fused<4>(q, k, v, o, batch, heads, seq_len, head_dim, causal, stream);
     if (rows_per_block == 64) return launch_fused<2>(q, k, v, o, batch, heads, seq_len, head_dim, causal, stream);
+    if (rows_per_block == 256)
+        return launch_fused<8, 1>(q, k, v, o, batch, heads, seq_len, head_dim, causal, stream);
     return hipErrorInvalidValue;
 }
 
@@ -1061,6 +1121,14 @@ int fa_launch_attention_tensorcore_v3(const void* q, const void* k, const void* 
 }
 
 int fa_query_tensorcore_v3(int head_dim, fa_tiling_info* info) { return query_fused<4>(head_dim, info); }
+
+int fa_query_fused(int head_dim, int rows_per_block, fa_tiling_info* info)
+{
+    if (rows_per_block == 128) return query_fused<4>(head_dim, info);
+    if (rows_per_block == 64) return query_fused<2>(head_dim, info);
+    if (rows_per_block == 256) return query_fused<8, 1>(head_dim, info);
+    return hipErrorInvalidValue;
+}
 
 double fa_tensorcore_v3_hbm_bytes(int batch, int heads, int seq_len, int head_dim, int causal)
 {

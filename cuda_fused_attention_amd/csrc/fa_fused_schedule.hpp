@@ -86,4 +86,16 @@ FA_HD inline FusedSplit fused_split(int n_tiles)
     return s;
 }
 
+// The same walk for a workgroup with one wave group (no split of the KV
+// range): group 0 takes every tile.
+FA_HD inline FusedSplit fused_single(int n_tiles)
+{
+    FusedSplit s;
+    s.count0 = n_tiles;
+    s.first1 = n_tiles;
+    s.count1 = 0;
+    s.barriers = fused_group_barriers(0, n_tiles);
+    return s;
+}
+
 }  // namespace fa

@@ -103,12 +103,20 @@ int fa_launch_attention_tensorcore_v3(const void* q, const void* k, const void* 
 
 /* No counterpart in the reference (whose v3 has one tile configuration): the
  * fused forward with an explicit workgroup configuration. rows_per_block is
- * 128 (the v3 configuration), 64 (the v3b configuration) or 0 (the choice
- * fa_launch_attention_tensorcore_v3 makes); anything else returns
+ * 128 (the v3 configuration: two wave groups split the KV range), 64 (the
+ * v3b configuration), 256 (head_dim 128 only: one group of 8 waves walks the
+ * whole KV range, half the L2->LDS copies per score, for grids with many
+ * workgroups per CU) or 0 (the choice fa_launch_attention_tensorcore_v3
+ * makes); anything else, or 256 with head_dim 64, returns
  * hipErrorInvalidValue. For callers and tests that pin the configuration. */
 int fa_launch_attention_fused(const void* q, const void* k, const void* v, void* o,
                               int batch, int heads, int seq_len, int head_dim,
                               int causal, int rows_per_block, void* stream);
+
+/* No counterpart in the reference: fa_query_tensorcore_v3 for the
+ * configuration fa_launch_attention_fused runs with rows_per_block (64, 128
+ * or 256). */
+int fa_query_fused(int head_dim, int rows_per_block, fa_tiling_info* info);
 
 /* include/flash_attention.h:94, kernels/v3/v3_tensorcore.cu:752-790 */
 int fa_query_tensorcore_v3(int head_dim, fa_tiling_info* info);
@@ -131,7 +139,8 @@ double fa_tensorcore_v3b_hbm_bytes(int batch, int heads, int seq_len, int head_d
 
 /* Harness support (benchmarks/bench_flash_attention.cu:265-299): run
  * `warmup` untimed launches of kernel `which` (0 = unfused, 1 = v3 fused,
- * 2 = v3b fused, 3 = fused with 128 rows per workgroup whatever the shape),
+ * 2 = v3b fused, 3 = fused with 128 rows per workgroup whatever the shape,
+ * 4 = fused with 256 rows per workgroup),
  * synchronise, then `iters` launches each bracketed by
  * hipEventRecord on `stream`; elapsed milliseconds go to samples_ms[iters].
  * Returns FA_ERROR_UNSUPPORTED for an unsupported head_dim and

@@ -50,6 +50,11 @@ def run(fa, kernel: str, q, k, v, causal: bool, stream=None, out=None):
         assert fa.launch_attention_tensorcore_v3b(q, k, v, o, shape, causal, stream=st)
     elif kernel == "v3_128":
         assert fa.launch_attention_fused(q, k, v, o, shape, causal, rows_per_block=128, stream=st)
+    elif kernel == "v3_256":
+        # The one-group 256-row configuration exists for head_dim 128 only;
+        # at head_dim 64 this runs the 128-row one.
+        rows = 256 if shape.head_dim == 128 else 128
+        assert fa.launch_attention_fused(q, k, v, o, shape, causal, rows_per_block=rows, stream=st)
     else:
         raise ValueError(kernel)
     torch.cuda.synchronize()
@@ -62,6 +67,6 @@ def run_bits(fa, kernel, qb, kb, vb, causal):
 
 
 # v3_mfma picks its workgroup configuration from the shape (64 rows for
-# grids that leave CUs idle); v3_128 pins the 128-row one, so small shapes
-# still exercise it.
-KERNELS = ["v0_unfused", "v3_mfma", "v3b_mfma", "v3_128"]
+# grids that leave CUs idle); v3_128 and v3_256 pin the 128-row and the
+# one-group 256-row ones, so every shape exercises each.
+KERNELS = ["v0_unfused", "v3_mfma", "v3b_mfma", "v3_128", "v3_256"]

@@ -116,7 +116,7 @@ def test_causal_work_layouts(fa, oracle_mod):
     for (B, H, N, D) in cases:
         q, k, v = oracle_mod.make_inputs(B, H, N, D, seeds={"q": 41, "k": 42, "v": 43})
         ref = oracle_mod.attention(q, k, v, True, threads=HOST_THREADS)
-        for kernel in ("v3_mfma", "v3b_mfma", "v3_128"):
+        for kernel in ("v3_mfma", "v3b_mfma", "v3_128", "v3_256"):
             say("causal layout", kernel, B, H, N, D)
             check(oracle_mod, run_bits(fa, kernel, q, k, v, True), ref, f"causal layout {kernel} {(B, H, N, D)}")
 
@@ -149,7 +149,7 @@ def test_base_moves(fa, oracle_mod):
             for name, qq, kk, vv in cases:
                 for causal in (False, True):
                     ref = oracle_mod.attention(qq, kk, vv, causal, threads=HOST_THREADS)
-                    for kernel in ("v3_mfma", "v3b_mfma", "v3_128"):
+                    for kernel in ("v3_mfma", "v3b_mfma", "v3_128", "v3_256"):
                         say("base moves", name, kernel, N, D, causal)
                         check(oracle_mod, run_bits(fa, kernel, qq, kk, vv, causal), ref,
                               f"base moves {name} {kernel} {(N, D, causal)}")
@@ -184,16 +184,23 @@ def test_v3_and_v3b_agree(fa, oracle_mod):
 
 def test_v3_picks_the_configuration_by_grid(fa, oracle_mod):
     """The v3 entry runs 64 rows per workgroup when the 128-row grid has fewer
-    workgroups than the device has CUs, else 128: its output equals the
-    pinned configuration's bit for bit (dense and causal), on each side of
-    the threshold."""
+    workgroups than the device has CUs; 256 (one wave group, head_dim 128)
+    when even 256-row workgroups give every CU one (dense) or, causal, for
+    seq_len >= 8192 with two rounds of them; else 128. Its output equals the
+    pinned configuration's bit for bit on each side of each threshold."""
     cus = fa.query_tensorcore_v3(64)["compute_units"]
     assert cus > 0
-    below = (1, 2, 700, 64)                       # 2 * 6 = 12 workgroups of 128 rows
-    at = (1, cus // 2, 256, 64)                   # exactly `cus` workgroups of 128 rows
-    for (B, H, N, D), pinned in ((below, "v3b_mfma"), (at, "v3_128")):
+    cases = [
+        ((1, 2, 700, 64), (False, True), "v3b_mfma"),           # 12 workgroups of 128 rows
+        ((1, cus // 2, 256, 64), (False, True), "v3_128"),      # `cus` of 128 rows, head_dim 64
+        ((1, cus // 2, 256, 128), (False, True), "v3_128"),     # `cus` of 128 rows, `cus`/2 of 256
+        ((1, cus, 256, 128), (False,), "v3_256"),               # `cus` workgroups of 256 rows, dense
+        ((1, 2 * cus // 32, 8192, 128), (True,), "v3_256"),     # causal, 2 * `cus` of 256 rows
+        ((1, 4 * cus // 16, 4096, 128), (True,), "v3_128"),     # causal below 8192 keys
+    ]
+    for (B, H, N, D), masks, pinned in cases:
         q, k, v = (to_dev(x) for x in oracle_mod.make_inputs(B, H, N, D))
-        for causal in (False, True):
+        for causal in masks:
             say("v3 dispatch", B, H, N, D, causal, pinned)
             a = from_dev(run(fa, "v3_mfma", q, k, v, causal))
             b = from_dev(run(fa, pinned, q, k, v, causal))
@@ -304,8 +311,12 @@ def test_error_paths_leave_output_untouched(fa, oracle_mod):
 
 
 def test_query_reports_resources(fa):
+    wide = fa.query_fused(128, 256)
+    assert wide["rows_per_block"] == 256 and wide["waves_per_block"] == 8 and wide["block_size"] == 512
+    assert fa.query_fused(64, 256)["supported"] == 0
     for d in (64, 128):
-        for info in (fa.query_tensorcore_v3(d), fa.query_tensorcore_v3b(d)):
+        infos = [fa.query_tensorcore_v3(d), fa.query_tensorcore_v3b(d)] + ([wide] if d == 128 else [])
+        for info in infos:
             print(d, info)
             assert info["supported"] == 1
             assert info["registers_per_thread"] > 0
