@@ -32,7 +32,7 @@ KERNEL_UNFUSED = 0
 KERNEL_V3 = 1
 KERNEL_V3B = 2
 KERNEL_V3_128 = 3  # the fused forward pinned to 128 rows per workgroup
-KERNEL_V3_256 = 4  # pinned to 256 rows per workgroup (one wave group; head_dim 128)
+KERNEL_V3_256 = 4  # pinned to 256 rows per workgroup (one wave group)
 KERNEL_IDS = {"v0_unfused": KERNEL_UNFUSED, "v3_mfma": KERNEL_V3, "v3b_mfma": KERNEL_V3B, "v3_128": KERNEL_V3_128,
               "v3_256": KERNEL_V3_256}
 
@@ -261,8 +261,8 @@ def launch_attention_tensorcore_v3(q, k, v, o, shape, causal: bool, stream=None)
 
 def launch_attention_fused(q, k, v, o, shape, causal: bool, rows_per_block: int = 0, stream=None) -> bool:
     """The fused forward with a pinned workgroup configuration (no counterpart in
-    the reference): rows_per_block 128 (v3), 64 (v3b), 256 (one wave group, head_dim
-    128) or 0 (the v3 entry's choice)."""
+    the reference): rows_per_block 128 (v3), 64 (v3b), 256 (one wave group) or 0
+    (the v3 entry's choice)."""
     s = _shape_of(shape)
     st = lib().fa_launch_attention_fused(_ptr(q), _ptr(k), _ptr(v), _ptr(o), s.batch, s.heads, s.seq_len,
                                          s.head_dim, int(causal), int(rows_per_block), _stream(stream))

@@ -92,11 +92,16 @@ constexpr int kStages = fa::kFusedStages;  // LDS stages per tensor per group
 constexpr float kSumLimit = 256.0f;        // a tile's partial row sum above this moves the exponent base
 
 // How the kWpg waves of one group share the copies of a K or V tile.
+// A copy moves 1 KiB (64 lanes x 16 B), or 512 B from the low 32 lanes when
+// a tile has fewer 1 KiB pieces than the group has waves (head_dim 64 with 8
+// waves), so that every wave issues the same number of copies.
 template <int D, int kWpg>
 struct TileCopy
 {
     static constexpr int kChunks = D / 8;                              // 16-byte chunks per row
-    static constexpr int kRowsPerIssue = 64 / kChunks;                 // rows one 64-lane DMA covers
+    static constexpr int kLanes = kTileKV * D * 2 / 1024 >= kWpg ? 64 : 32;  // lanes per copy
+    static constexpr int kCopyBytes = 16 * kLanes;
+    static constexpr int kRowsPerIssue = kLanes / kChunks;             // rows one copy covers
     static constexpr int kIssues = kTileKV / (kRowsPerIssue * kWpg);   // DMA issues per wave per tile
     static_assert(kIssues >= 1 && kIssues * kRowsPerIssue * kWpg == kTileKV, "tile splits evenly over a group");
 };
@@ -115,6 +120,7 @@ struct Cfg : TileCopy<D, kWpg>
     static constexpr int kLdsElems = kGroups * kGroupElems;
     static constexpr int kQElems = kWpg * 32 * D;                      // Q rows of the kWpg slots
     static constexpr int kQIssues = 32 * D * 2 / 1024;                 // DMA issues per slot's Q rows
+    static constexpr int kQRowsPerIssue = 64 / (D / 8);                // rows one (64-lane) Q copy covers
     static constexpr int kQIssuesPerWave = kQIssues / kGroups;
     static_assert(D == 64 || D == 128, "head_dim 64 or 128");
     static_assert(kGroups == 1 || kGroups == 2, "one or two wave groups");
@@ -212,11 +218,12 @@ __device__ __forceinline__ uint32_t lds_addr(const uint16_t* p)
 }
 
 // Per-lane byte offsets (from a tile's first row) of this wave's DMA copies
-// of one K or V tile (kIssues copies of 64 x 16 B): copy u covers tile rows
-// [row0, row0 + kRowsPerIssue) with row0 = (u*kWpg + wg) * kRowsPerIssue;
-// lane l fetches row row0 + l / kChunks, and its logical 16-byte chunk is
-// chosen so that the chunk lands at its swizzled position (the copy writes
-// lane l's 16 bytes to LDS byte 16*l of the copy's 1 KiB block).
+// of one K or V tile (kIssues copies of kLanes x 16 B): copy u covers tile
+// rows [row0, row0 + kRowsPerIssue) with row0 = (u*kWpg + wg) *
+// kRowsPerIssue; lane l < kLanes fetches row row0 + l / kChunks, and its
+// logical 16-byte chunk is chosen so that the chunk lands at its swizzled
+// position (the copy writes lane l's 16 bytes to LDS byte 16*l of the copy's
+// block). Lanes past kLanes get offsets too but issue nothing.
 template <int D, int kWpg, bool kIsV>
 __device__ __forceinline__ void dma_lane_offsets(int wg, int lane, uint32_t (&voff)[TileCopy<D, kWpg>::kIssues])
 {
@@ -251,10 +258,13 @@ __device__ __forceinline__ i32x4 tile_rsrc(ScalarPtr slab, int kv0, int n)
 
 // Copy u of this wave's share of one K or V tile.
 template <int D, int kWpg>
-__device__ __forceinline__ void dma_copy(i32x4 rsrc, uint32_t stage_lds, int wg_s, int u,
+__device__ __forceinline__ void dma_copy(i32x4 rsrc, uint32_t stage_lds, int wg_s, int u, int lane,
                                          const uint32_t (&voff)[TileCopy<D, kWpg>::kIssues])
 {
-    dma16(rsrc, voff[u], stage_lds + (u * kWpg + wg_s) * 1024);
+    using C = TileCopy<D, kWpg>;
+    const uint32_t lds = stage_lds + (u * kWpg + wg_s) * C::kCopyBytes;
+    if constexpr (C::kLanes == 64) dma16(rsrc, voff[u], lds);
+    else if (lane < C::kLanes) dma16(rsrc, voff[u], lds);
 }
 
 template <int D>
@@ -535,10 +545,12 @@ __global__ __launch_bounds__(64 * kGroups * kWpg) void fused_attention_kernel(co
         dma_lane_offsets<D, kWpg, true>(wg, lane, voff);
         auto kv_at = [&](int jj) { return min(tb + jj, n_tiles - 1) * kTileKV; };
         auto copy_k = [&](int jj, int stage, int u) {
-            dma_copy<D, kWpg>(tile_rsrc<D>(k_bytes, kv_at(jj), n), k_lds + stage * (C::kTileElems * 2), wg_s, u, koff);
+            dma_copy<D, kWpg>(tile_rsrc<D>(k_bytes, kv_at(jj), n), k_lds + stage * (C::kTileElems * 2), wg_s, u, lane,
+                              koff);
         };
         auto copy_v = [&](int jj, int stage, int u) {
-            dma_copy<D, kWpg>(tile_rsrc<D>(v_bytes, kv_at(jj), n), v_lds + stage * (C::kTileElems * 2), wg_s, u, voff);
+            dma_copy<D, kWpg>(tile_rsrc<D>(v_bytes, kv_at(jj), n), v_lds + stage * (C::kTileElems * 2), wg_s, u, lane,
+                              voff);
         };
 
         // Prologue: the wave's Q rows first, then K_0 .. K_{S-1},
@@ -560,7 +572,7 @@ __global__ __launch_bounds__(64 * kGroups * kWpg) void fused_attention_kernel(co
                 const int qs = j / C::kQIssues;  // slot whose rows this copy moves
                 const int u = j % C::kQIssues;
                 const int row0 = slot_row0(qs);
-                const int row = u * C::kRowsPerIssue + sub_row;
+                const int row = u * C::kQRowsPerIssue + sub_row;
                 const uint32_t voff = static_cast<uint32_t>(row * (D * 2) + ((pchunk ^ swz_k<D>(row)) * 16));
                 const uint32_t bytes = row0 < n ? static_cast<uint32_t>((n - row0) * (D * 2)) : 0u;
                 const i32x4 rsrc = make_rsrc(q_bytes, static_cast<uint32_t>(min(row0, n) * (D * 2)), bytes);
@@ -922,11 +934,7 @@ const void* kernel_ptr()
 template <int kWpg, int kGroups>
 const void* pick_kernel(int head_dim, bool causal)
 {
-    if (head_dim == 64)
-    {
-        if constexpr (kGroups == 1) return nullptr;  // a 4 KiB tile does not split over 8 waves' 1 KiB copies
-        else return causal ? kernel_ptr<64, kWpg, true, kGroups>() : kernel_ptr<64, kWpg, false, kGroups>();
-    }
+    if (head_dim == 64) return causal ? kernel_ptr<64, kWpg, true, kGroups>() : kernel_ptr<64, kWpg, false, kGroups>();
     if (head_dim == 128)
         return causal ? kernel_ptr<128, kWpg, true, kGroups>() : kernel_ptr<128, kWpg, false, kGroups>();
     return nullptr;
@@ -963,7 +971,6 @@ int launch_fused(const void* q, const void* k, const void* v, void* o, int batch
                  int head_dim, int causal, void* stream_ptr)
 {
     if (head_dim != 64 && head_dim != 128) return FA_ERROR_UNSUPPORTED;
-    if (kGroups == 1 && head_dim != 128) return hipErrorInvalidValue;
     if (batch < 0 || heads < 0 || seq_len < 0) return hipErrorInvalidValue;
     const long long bh = static_cast<long long>(batch) * heads;
     if (bh == 0 || seq_len == 0) return hipSuccess;
@@ -997,11 +1004,8 @@ int launch_fused(const void* q, const void* k, const void* v, void* o, int batch
     const int tot = static_cast<int>(total);
     if (head_dim == 64)
     {
-        if constexpr (kGroups == 2)
-        {
-            if (causal) launch_typed<64, kWpg, true, kGroups>(qb, kb, vb, ob, seq_len, qbk, tot, c_log2, paired, stream);
-            else launch_typed<64, kWpg, false, kGroups>(qb, kb, vb, ob, seq_len, qbk, tot, c_log2, 0, stream);
-        }
+        if (causal) launch_typed<64, kWpg, true, kGroups>(qb, kb, vb, ob, seq_len, qbk, tot, c_log2, paired, stream);
+        else launch_typed<64, kWpg, false, kGroups>(qb, kb, vb, ob, seq_len, qbk, tot, c_log2, 0, stream);
     }
     else
     {
@@ -1015,22 +1019,22 @@ int launch_fused(const void* q, const void* k, const void* v, void* o, int batch
 // MI355X):
 //   * 64 when the 128-row grid has fewer workgroups than CUs (small
 //     batch*heads*seq_len): twice as many workgroups finish sooner;
-//   * 256 (one wave group, head_dim 128) when even 256-row workgroups give
-//     every CU one (dense), or, causal, for seq_len >= 8192 with at least two
-//     rounds of them: half the L2->LDS copies per score and no merge, 4-7%
-//     faster there; shorter causal sequences lose more to the coarser
-//     diagonal blocks than they gain;
+//   * 256 (one wave group) when even 256-row workgroups give every CU one
+//     (dense), or, causal, for seq_len >= 8192 with at least two rounds of
+//     them: half the L2->LDS copies per score and no merge, 2-7% faster
+//     there; shorter causal sequences lose more to the coarser diagonal
+//     blocks than they gain;
 //   * 128 otherwise.
 // Dense outputs of the 64- and 128-row configurations are bitwise identical
 // (each wave computes its 32 rows the same way in both).
-int auto_rows_per_block(int batch, int heads, int seq_len, int head_dim, int causal)
+int auto_rows_per_block(int batch, int heads, int seq_len, int causal)
 {
     if (batch <= 0 || heads <= 0 || seq_len <= 0) return 128;
     const long long bh = static_cast<long long>(batch) * heads;
     const long long cus = device_compute_units();
     if (bh * ((static_cast<long long>(seq_len) + 127) / 128) < cus) return 64;
     const long long wide = bh * ((static_cast<long long>(seq_len) + 255) / 256);
-    if (head_dim == 128 && (causal ? (seq_len >= 8192 && wide >= 2 * cus) : wide >= cus)) return 256;
+    if (causal ? (seq_len >= 8192 && wide >= 2 * cus) : wide >= cus) return 256;
     return 128;
 }
 
@@ -1106,7 +1110,7 @@ int fa_tensorcore_v3_supported(int head_dim) { return head_dim == 64 || head_dim
 int fa_launch_attention_fused(const void* q, const void* k, const void* v, void* o, int batch, int heads,
                               int seq_len, int head_dim, int causal, int rows_per_block, void* stream)
 {
-    if (rows_per_block == 0) rows_per_block = auto_rows_per_block(batch, heads, seq_len, head_dim, causal);
+    if (rows_per_block == 0) rows_per_block = auto_rows_per_block(batch, heads, seq_len, causal);
     if (rows_per_block == 128) return launch_fused<4>(q, k, v, o, batch, heads, seq_len, head_dim, causal, stream);
     if (rows_per_block == 64) return launch_fused<2>(q, k, v, o, batch, heads, seq_len, head_dim, causal, stream);
     if (rows_per_block == 256)

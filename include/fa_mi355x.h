@@ -104,11 +104,11 @@ int fa_launch_attention_tensorcore_v3(const void* q, const void* k, const void* 
 /* No counterpart in the reference (whose v3 has one tile configuration): the
  * fused forward with an explicit workgroup configuration. rows_per_block is
  * 128 (the v3 configuration: two wave groups split the KV range), 64 (the
- * v3b configuration), 256 (head_dim 128 only: one group of 8 waves walks the
- * whole KV range, half the L2->LDS copies per score, for grids with many
- * workgroups per CU) or 0 (the choice fa_launch_attention_tensorcore_v3
- * makes); anything else, or 256 with head_dim 64, returns
- * hipErrorInvalidValue. For callers and tests that pin the configuration. */
+ * v3b configuration), 256 (one group of 8 waves walks the whole KV range:
+ * half the L2->LDS copies per score, for grids with many workgroups per CU)
+ * or 0 (the choice fa_launch_attention_tensorcore_v3 makes); anything else
+ * returns hipErrorInvalidValue. For callers and tests that pin the
+ * configuration. */
 int fa_launch_attention_fused(const void* q, const void* k, const void* v, void* o,
                               int batch, int heads, int seq_len, int head_dim,
                               int causal, int rows_per_block, void* stream);

@@ -51,10 +51,7 @@ def run(fa, kernel: str, q, k, v, causal: bool, stream=None, out=None):
     elif kernel == "v3_128":
         assert fa.launch_attention_fused(q, k, v, o, shape, causal, rows_per_block=128, stream=st)
     elif kernel == "v3_256":
-        # The one-group 256-row configuration exists for head_dim 128 only;
-        # at head_dim 64 this runs the 128-row one.
-        rows = 256 if shape.head_dim == 128 else 128
-        assert fa.launch_attention_fused(q, k, v, o, shape, causal, rows_per_block=rows, stream=st)
+        assert fa.launch_attention_fused(q, k, v, o, shape, causal, rows_per_block=256, stream=st)
     else:
         raise ValueError(kernel)
     torch.cuda.synchronize()

@@ -89,9 +89,7 @@ def test_argument_validation_before_launch(fa_lib):
     # the pinned-configuration entry: only 0 (auto), 64 and 128 rows per workgroup
     for rows in (-1, 1, 32, 96, 512):
         assert L.fa_launch_attention_fused(fake, fake, fake, fake, 1, 1, 64, 64, 0, rows, None) == 1
-    # the one-group 256-row configuration exists for head_dim 128 only
-    assert L.fa_launch_attention_fused(fake, fake, fake, fake, 1, 1, 64, 64, 0, 256, None) == 1
-    assert L.fa_launch_attention_fused(None, None, None, None, 0, 8, 64, 128, 1, 256, None) == 0
+    assert L.fa_launch_attention_fused(None, None, None, None, 0, 8, 64, 64, 1, 256, None) == 0
     for rows in (0, 64, 128, 256):
         assert L.fa_launch_attention_fused(fake, fake, fake, fake, 1, 1, 64, 96, 0, rows, None) == fa_lib.FA_ERROR_UNSUPPORTED
         assert L.fa_launch_attention_fused(None, None, None, None, 0, 8, 64, 128, 1, rows, None) == 0

@@ -184,9 +184,9 @@ def test_v3_and_v3b_agree(fa, oracle_mod):
 
 def test_v3_picks_the_configuration_by_grid(fa, oracle_mod):
     """The v3 entry runs 64 rows per workgroup when the 128-row grid has fewer
-    workgroups than the device has CUs; 256 (one wave group, head_dim 128)
-    when even 256-row workgroups give every CU one (dense) or, causal, for
-    seq_len >= 8192 with two rounds of them; else 128. Its output equals the
+    workgroups than the device has CUs; 256 (one wave group) when even
+    256-row workgroups give every CU one (dense) or, causal, for seq_len >=
+    8192 with two rounds of them; else 128. Its output equals the
     pinned configuration's bit for bit on each side of each threshold."""
     cus = fa.query_tensorcore_v3(64)["compute_units"]
     assert cus > 0
@@ -195,6 +195,7 @@ def test_v3_picks_the_configuration_by_grid(fa, oracle_mod):
         ((1, cus // 2, 256, 64), (False, True), "v3_128"),      # `cus` of 128 rows, head_dim 64
         ((1, cus // 2, 256, 128), (False, True), "v3_128"),     # `cus` of 128 rows, `cus`/2 of 256
         ((1, cus, 256, 128), (False,), "v3_256"),               # `cus` workgroups of 256 rows, dense
+        ((1, cus, 256, 64), (False,), "v3_256"),
         ((1, 2 * cus // 32, 8192, 128), (True,), "v3_256"),     # causal, 2 * `cus` of 256 rows
         ((1, 4 * cus // 16, 4096, 128), (True,), "v3_128"),     # causal below 8192 keys
     ]
@@ -311,11 +312,10 @@ def test_error_paths_leave_output_untouched(fa, oracle_mod):
 
 
 def test_query_reports_resources(fa):
-    wide = fa.query_fused(128, 256)
-    assert wide["rows_per_block"] == 256 and wide["waves_per_block"] == 8 and wide["block_size"] == 512
-    assert fa.query_fused(64, 256)["supported"] == 0
     for d in (64, 128):
-        infos = [fa.query_tensorcore_v3(d), fa.query_tensorcore_v3b(d)] + ([wide] if d == 128 else [])
+        wide = fa.query_fused(d, 256)
+        assert wide["rows_per_block"] == 256 and wide["waves_per_block"] == 8 and wide["block_size"] == 512
+        infos = [fa.query_tensorcore_v3(d), fa.query_tensorcore_v3b(d), wide]
         for info in infos:
             print(d, info)
             assert info["supported"] == 1
