@@ -5,17 +5,20 @@
 //
 // Work layout (CDNA4-first, not a translation of the m16n8k16 design):
 //
-//   * A workgroup owns 32*kWpg query rows and runs two wave groups of kWpg
-//     wave64s each. Wave w of group 0 and wave w of group 1 own the same 32
-//     rows; group 0 walks the first half of the KV tiles, group 1 the second
-//     half (split-KV inside the workgroup), and their partial (max, sum, O)
-//     are merged through LDS at the end. This keeps 128-row workgroups (one
-//     per CU at (2,8,2048,D)) while giving every SIMD two waves.
+//   * A workgroup owns 32*kWpg query rows and runs kGroups wave groups of
+//     kWpg wave64s each. With two groups, wave w of group 0 and wave w of
+//     group 1 own the same 32 rows; group 0 walks the first half of the KV
+//     tiles, group 1 the second half (split-KV inside the workgroup), and
+//     their partial (max, sum, O) are merged through LDS at the end. This
+//     keeps 128-row workgroups (one per CU at (2,8,2048,D)) while giving
+//     every SIMD two waves. With one group (8 waves, 256 rows, for grids
+//     with many workgroups per CU) every wave walks the whole KV range on
+//     one tile stream: half the copies per score and no merge.
 //   * Both GEMMs use v_mfma_f32_32x32x16_bf16. QK^T is computed transposed,
 //     S^T = K . Q^T (K tile = A operand, the wave's Q rows in registers = B
 //     operand): lane l then holds query l % 32 and keys 8*(r/4) + 4*(l/32) +
 //     r%4 of a 32-key tile, so a row's max and sum need one cross-lane step
-//     (v_permlane32_swap). PV is computed as O^T = V^T . P^T: the
+//     (v_permlane32_swap, or a shuffle for the final sum). PV is computed as O^T = V^T . P^T: the
 //     exponentiated scores already are the B operand, P never leaves
 //     registers, and O^T's layout again gives lane l query l % 32, so the
 //     online-softmax rescale is per lane. The A operand (8 keys of one head
@@ -59,11 +62,12 @@
 //     Every P the matrix pipe consumes is <= 256.
 //   * Causal: a wave skips tiles wholly above its diagonal, and only tiles
 //     that cross the diagonal or the sequence end pay for the per-element
-//     mask (-inf). A workgroup owns two half blocks of rows, an early one and
-//     its mirror from the end of the sequence, so all workgroups carry about
-//     the same number of (row, key) pairs instead of the last one carrying a
-//     full dense row of tiles; within each SIMD one wave holds early rows and
-//     one late rows.
+//     mask (-inf). When the grid fits one round on the device, a two-group
+//     workgroup owns two half blocks of rows, an early one and its mirror
+//     from the end of the sequence, so all workgroups carry about the same
+//     number of (row, key) pairs instead of the last one carrying a full
+//     dense row of tiles; within each SIMD one wave holds early rows and one
+//     late rows. Larger grids keep whole blocks, issued heaviest first.
 //   * Workgroup ids are remapped so that all query blocks of a (batch, head)
 //     slab run on one XCD and share its L2 (measured: K and V are read from
 //     HBM once).
