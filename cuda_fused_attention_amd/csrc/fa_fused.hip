@@ -405,9 +405,28 @@ __device__ __forceinline__ void mask_tile(f32x16& s, int limit)
         if (8 * (r >> 2) + (r & 3) >= limit) s[r] = -INFINITY;
 }
 
+// Both lane halves' values of a row: v_permlane32_swap of two copies of x
+// swaps lanes 32-63 of the first with lanes 0-31 of the second, leaving
+// {own, partner} (lanes < 32) or {partner, own} (lanes >= 32) in the pair.
+// Issued as inline asm with both registers as outputs: the compiler's
+// builtin for it keeps only the first register's result (it read the first
+// result twice), which silently returned the lane's own half. The s_nop
+// gives the two wait states a VALU write needs before the swap reads it.
+__device__ __forceinline__ void row_halves(float x, float& a, float& b)
+{
+    uint32_t lo = __builtin_bit_cast(uint32_t, x);
+    uint32_t hi = lo;
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(lo), "+v"(hi));
+#pragma clang diagnostic pop
+    a = __builtin_bit_cast(float, lo);
+    b = __builtin_bit_cast(float, hi);
+}
+
 // Raw (unscaled) row max of a tile's scores: a v_maximum3_f32 tree over
 // the lane's 16 values (IEEE maximum needs no operand canonicalisation),
-// then the other half of the row from lane l^32 (v_permlane32_swap).
+// then the other half of the row from lane l^32 (row_halves).
 __device__ __forceinline__ float row_max_raw(const f32x16& s)
 {
     auto max3 = [](float a, float b, float c) {
@@ -419,9 +438,9 @@ __device__ __forceinline__ float row_max_raw(const f32x16& s)
     const float a3 = max3(s[9], s[10], s[11]);
     const float a4 = max3(s[12], s[13], s[14]);
     const float mx = __builtin_elementwise_maximum(max3(a0, a1, a2), max3(a3, a4, s[15]));
-    const uint32_t bits = __builtin_bit_cast(uint32_t, mx);
-    const auto swapped = __builtin_amdgcn_permlane32_swap(bits, bits, false, false);
-    return __builtin_elementwise_maximum(__builtin_bit_cast(float, swapped[0]), __builtin_bit_cast(float, swapped[1]));
+    float a, b;
+    row_halves(mx, a, b);
+    return __builtin_elementwise_maximum(a, b);
 }
 
 template <int D>
@@ -853,10 +872,15 @@ __global__ __launch_bounds__(64 * kGroups * kWpg) void fused_attention_kernel(co
         }
     };
 
-    // The two lane halves hold partial row sums of the same query.
+    // The two lane halves hold partial row sums of the same query
+    // (row_halves: no LDS round trip), and v_rcp_f32 (about 1 ulp of fp32,
+    // far below the bf16 rounding that follows) replaces the IEEE division
+    // sequence.
     auto inv_row_sum = [&](float l) {
-        const float l_tot = l + __shfl_xor(l, 32, 64);
-        return l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+        float a, b;
+        row_halves(l, a, b);
+        const float l_tot = a + b;
+        return l_tot > 0.0f ? __builtin_amdgcn_rcpf(l_tot) : 0.0f;
     };
 
     if constexpr (kGroups == 1)
