@@ -75,6 +75,18 @@ def measure_shape(fa, dev, B, H, N, D, causal, kernel, ws=None):
     return out
 
 
+def cpu_model() -> str:
+    """The host CPU's model name (Linux /proc/cpuinfo), or "unknown"."""
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(host_inputs, B, H, N, D, causal):
     """The FP64 oracle (a C++ port of benchmarks/bench_flash_attention.cu:105-145)
     timed on this host: all rows of the workload on up to 16 threads (the GPU
@@ -109,6 +121,7 @@ def cpu_baseline(host_inputs, B, H, N, D, causal):
         "single_thread": {"value": runs_one * flops / (B * H) / t_one / 1e12, "unit": "TFLOP/s",
                           "sample": f"slab 0 ({N} rows) on 1 thread, {runs_one} runs in {t_one:.1f} s"},
         "host_cpus": os.cpu_count(),
+        "cpu_model": cpu_model(),
     }
 
 
