@@ -42,7 +42,14 @@ WORKLOADS = {
     "c2_causal": (2, 8, 2048, 64, True),
     "headline": (2, 8, 2048, 128, False),
     "c3": (2, 8, 2048, 128, True),
+    "c5": (1, 16, 16384, 128, True),
 }
+# Input family per workload: BASELINE's uniform[-1,1), or its long-sequence
+# stress family for c5 (Q, K ~ N(0, 3^2), V uniform).
+FAMILY = {"c5": "stress"}
+# The per-shape extras (v3, v3b and v0 medians) cover BASELINE's four
+# (2,8,2048,D) shapes.
+EXTRA_WORKLOADS = ("c2", "c2_causal", "headline", "c3")
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
 
 
@@ -51,10 +58,11 @@ def baseline_flops(B, H, N, D, causal):
     return f / 2.0 if causal else f
 
 
-def make_device_inputs(B, H, N, D):
+def make_device_inputs(B, H, N, D, family="uniform"):
     from cuda_fused_attention_amd import inputs
 
-    host = inputs.make_uniform_inputs(B, H, N, D)
+    make = inputs.make_stress_inputs if family == "stress" else inputs.make_uniform_inputs
+    host = make(B, H, N, D)
     return host, [inputs.to_device(x) for x in host]
 
 
@@ -90,7 +98,11 @@ def cpu_model() -> str:
 def cpu_baseline(host_inputs, B, H, N, D, causal):
     """The FP64 oracle (a C++ port of benchmarks/bench_flash_attention.cu:105-145)
     timed on this host: all rows of the workload on up to 16 threads (the GPU
-    box's CPU share), plus one slab on 1 thread (the reference's semantics)."""
+    box's CPU share), plus one slab on 1 thread (the reference's semantics).
+    For seq_len > 2048 it times a stratified row sample instead (every 8th row
+    of every slab; every 64th of slab 0 for the single thread) and
+    extrapolates the whole-workload time linearly in (row, key) pairs, as the
+    sample string says."""
     import numpy as np
 
     import oracle
@@ -98,6 +110,8 @@ def cpu_baseline(host_inputs, B, H, N, D, causal):
     q, k, v = host_inputs
     threads = max(1, min(16, os.cpu_count() or 1))
     flops = baseline_flops(B, H, N, D, causal)
+    if N > 2048:
+        return cpu_baseline_sampled(host_inputs, B, H, N, D, causal, threads, flops)
 
     def repeat(fn, min_s):
         runs, t0 = 0, time.perf_counter()
@@ -120,6 +134,55 @@ def cpu_baseline(host_inputs, B, H, N, D, causal):
                   f"on {threads} threads, {runs_all} runs in {t_all:.1f} s",
         "single_thread": {"value": runs_one * flops / (B * H) / t_one / 1e12, "unit": "TFLOP/s",
                           "sample": f"slab 0 ({N} rows) on 1 thread, {runs_one} runs in {t_one:.1f} s"},
+        "host_cpus": os.cpu_count(),
+        "cpu_model": cpu_model(),
+    }
+
+
+def cpu_baseline_sampled(host_inputs, B, H, N, D, causal, threads, flops):
+    import numpy as np
+
+    import oracle
+
+    q, k, v = host_inputs
+
+    def pairs(rows_in_slab):
+        return float(np.sum(rows_in_slab + 1)) if causal else float(len(rows_in_slab)) * N
+
+    def timed(rows, min_s):
+        runs, t0 = 0, time.perf_counter()
+        while True:
+            oracle.attention(q, k, v, causal, rows=rows, threads=threads)
+            runs += 1
+            elapsed = time.perf_counter() - t0
+            if elapsed >= min_s:
+                return runs, elapsed
+
+    total_pairs = pairs(np.arange(N)) * B * H
+    strided = np.arange(0, N, 8, dtype=np.int64)
+    rows_all = (np.arange(B * H, dtype=np.int64)[:, None] * N + strided[None, :]).ravel()
+    runs_all, t_all = timed(rows_all, 10.0)
+    est_all = t_all / runs_all * total_pairs / (pairs(strided) * B * H)
+    strided1 = np.arange(0, N, 64, dtype=np.int64)
+    runs_one, t_one = 0, time.perf_counter()
+    while True:
+        oracle.attention(q, k, v, causal, rows=strided1, threads=1)
+        runs_one += 1
+        if time.perf_counter() - t_one >= 3.0:
+            break
+    t_one = time.perf_counter() - t_one
+    est_one = t_one / runs_one * pairs(np.arange(N)) / pairs(strided1)
+    return {
+        "value": flops / est_all / 1e12,
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"every 8th row of all {B * H} slabs of ({B},{H},{N},{D}) {'causal' if causal else 'dense'} "
+                  f"on {threads} threads, {runs_all} runs in {t_all:.1f} s; whole-workload time "
+                  f"extrapolated linearly in (row, key) pairs: {est_all:.1f} s",
+        "single_thread": {"value": flops / (B * H) / est_one / 1e12, "unit": "TFLOP/s",
+                          "sample": f"every 64th row of slab 0 on 1 thread, {runs_one} runs in {t_one:.1f} s; "
+                                    f"one slab extrapolated to {est_one:.1f} s"},
         "host_cpus": os.cpu_count(),
         "cpu_model": cpu_model(),
     }
@@ -168,7 +231,8 @@ def main():
     props = torch.cuda.get_device_properties(0)
 
     B, H, N, D, causal = WORKLOADS[args.workload]
-    host_inputs, dev = make_device_inputs(B, H, N, D)
+    family = FAMILY.get(args.workload, "uniform")
+    host_inputs, dev = make_device_inputs(B, H, N, D, family)
     shape = fa.AttentionShape(B, H, N, D)
     o = torch.empty_like(dev[0])
     flops = baseline_flops(B, H, N, D, causal)
@@ -180,8 +244,10 @@ def main():
     shapes = None
     if not args.no_extras:
         shapes = {}
-        for name, (b, h, n, d, c) in WORKLOADS.items():
-            _, sdev = make_device_inputs(b, h, n, d) if (b, h, n, d) != (B, H, N, D) else (None, dev)
+        for name in EXTRA_WORKLOADS:
+            b, h, n, d, c = WORKLOADS[name]
+            same = (b, h, n, d) == (B, H, N, D) and family == "uniform"
+            _, sdev = (None, dev) if same else make_device_inputs(b, h, n, d)
             sh = fa.AttentionShape(b, h, n, d)
             entry = {"shape": [b, h, n, d], "causal": c}
             for kern in ("v3_mfma", "v3b_mfma"):
@@ -237,7 +303,9 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic: Q/K/V uniform[-1,1) rounded to bf16, SplitMix64 seeds 11/22/33, resident in HBM",
+        "data": ("synthetic: Q/K ~ N(0, 3^2) (Box-Muller) and V uniform[-1,1), rounded to bf16, SplitMix64 "
+                 "seeds 11/22/33, resident in HBM" if family == "stress" else
+                 "synthetic: Q/K/V uniform[-1,1) rounded to bf16, SplitMix64 seeds 11/22/33, resident in HBM"),
         "config": {
             "workload": f"{args.workload}: fused attention forward ({B},{H},{N},{D}) "
                         f"{'causal' if causal else 'dense'}, [B,H,N,D] bf16, fp32 accumulate",
@@ -270,10 +338,11 @@ def main():
     result["clock_ramp_launches"] = ramp_launches
     if shapes is not None:
         result["shapes"] = shapes
-        result["v0"] = {"bound": "hbm", "peak": PEAK_HBM_GBPS, "unit": "GB/s",
-                        "achieved": shapes[args.workload]["v0_unfused"]["hbm_gbps"],
-                        "frac": shapes[args.workload]["v0_unfused"]["hbm_frac"],
-                        "bytes_model": "16*B*H*N^2 + 8*B*H*N*D"}
+        if args.workload in shapes:
+            result["v0"] = {"bound": "hbm", "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                            "achieved": shapes[args.workload]["v0_unfused"]["hbm_gbps"],
+                            "frac": shapes[args.workload]["v0_unfused"]["hbm_frac"],
+                            "bytes_model": "16*B*H*N^2 + 8*B*H*N*D"}
 
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(host_inputs, B, H, N, D, causal)

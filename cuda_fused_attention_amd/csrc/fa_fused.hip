@@ -56,10 +56,10 @@
 //   * Scores stay in the log2 domain (scale*log2(e) folded into one FMA before
 //     v_exp_f32). Row sums accumulate the bf16-rounded P with
 //     v_dot2_f32_bf16, the same weights the PV MFMA uses. The exponent base
-//     is set from the first tile's row max; afterwards no per-tile row max is
-//     taken: the base is raised only when a tile's partial row sum exceeds
-//     2^8, and then O and the row sum are rescaled and the tile recomputed.
-//     Every P the matrix pipe consumes is <= 256.
+//     is set from the first tile's row max (plus headroom); afterwards no
+//     per-tile row max is taken: the base is raised only when a tile's
+//     partial row sum exceeds 2^16, and then O and the row sum are rescaled
+//     and the tile recomputed. Every P the matrix pipe consumes is <= 2^16.
 //   * Causal: a wave skips tiles wholly above its diagonal, and only tiles
 //     that cross the diagonal or the sequence end pay for the per-element
 //     mask (-inf). When the grid fits one round on the device, a two-group
@@ -93,7 +93,17 @@ typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
 constexpr int kTileKV = fa::kFusedTileKV;  // keys per LDS tile
 constexpr int kStages = fa::kFusedStages;  // LDS stages per tensor per group
-constexpr float kSumLimit = 256.0f;        // a tile's partial row sum above this moves the exponent base
+// A tile's partial row sum above kSumLimit moves the exponent base; a new
+// base is placed kBaseHeadroom (log2 units) above the row max, so a row's
+// max must grow by about kBaseHeadroom + 12 before the next move. Every P is
+// then at most 2^16, and after a move at most 2^-48: that leaves 78 binary
+// orders of magnitude below the row max before fp32 denormals, and keys
+// further down weigh less than 2^-78 of the largest. Moves are expensive
+// (the tile is recomputed), and inputs with large, still-growing logits
+// (N(0, 3^2) Q and K) made them frequent with a tight limit and no headroom:
+// c5 went from 1.40 ms to 0.955 ms with these values.
+constexpr float kSumLimit = 65536.0f;
+constexpr float kBaseHeadroom = 48.0f;
 
 // How the kWpg waves of one group share the copies of a K or V tile.
 // A copy moves 1 KiB (64 lanes x 16 B), or 512 B from the low 32 lanes when
@@ -661,7 +671,7 @@ __global__ __launch_bounds__(64 * kGroups * kWpg) void fused_attention_kernel(co
             qk_part<D, 0, D / 16>(f, ka, sbuf[0]);
             if (tb >= t_mask) mask_tile(sbuf[0], dead_base - tb * kTileKV);
             // O and l are still zero: the base moves without rescaling.
-            rs.m = __builtin_elementwise_maximum(rs.m, row_max_raw(sbuf[0]) * c_log2);
+            rs.m = __builtin_elementwise_maximum(rs.m, row_max_raw(sbuf[0]) * c_log2 + kBaseHeadroom);
             exp_part<0, 0, 8>(sbuf[0], p_lo[0], rs.m, c_log2, tsum);
         }
         wait_vm_lgkm0<0>();
@@ -715,7 +725,7 @@ __global__ __launch_bounds__(64 * kGroups * kWpg) void fused_attention_kernel(co
                 __builtin_amdgcn_sched_barrier(0);
             }
             if (t >= t_mask) mask_tile(st, dead_base - t * kTileKV);
-            const float m_new = __builtin_elementwise_maximum(rs.m, row_max_raw(st) * c_log2);
+            const float m_new = __builtin_elementwise_maximum(rs.m, row_max_raw(st) * c_log2 + kBaseHeadroom);
             const float alpha = __builtin_amdgcn_exp2f(rs.m - m_new);
             rs.m = m_new;
             rescale_o<D>(f, alpha);

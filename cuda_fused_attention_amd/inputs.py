@@ -52,6 +52,31 @@ def fill_uniform(shape, seed: int, chunk: int = 1 << 22) -> np.ndarray:
     return out.reshape(shape)
 
 
+def fill_normal(shape, seed: int, sigma: float = 1.0, chunk: int = 1 << 21) -> np.ndarray:
+    """bf16 bit patterns of `shape`, N(0, sigma^2) by Box-Muller on SplitMix64(seed):
+    draw i takes outputs 2i and 2i+1 as u1, u2 on the 2^-53 grid and gives
+    sigma * sqrt(-2 log(1 - u1)) * cos(2 pi u2) in binary64, rounded to binary32, then to bf16 (RNE)."""
+    n = int(np.prod(shape))
+    out = np.empty(n, dtype=np.uint16)
+    two_pi = 6.283185307179586
+    for start in range(0, n, chunk):
+        m = min(chunk, n - start)
+        z = _splitmix64(seed, 2 * m, 2 * start)
+        u = (z >> np.uint64(11)).astype(np.float64) * (2.0 ** -53)
+        radius = np.sqrt(-2.0 * np.log1p(-u[0::2]))
+        out[start:start + m] = _f32_to_bf16_bits((sigma * radius * np.cos(two_pi * u[1::2])).astype(np.float32))
+    return out.reshape(shape)
+
+
+def make_stress_inputs(batch: int, heads: int, seq_len: int, head_dim: int, seeds=None):
+    """BASELINE's long-sequence stress family: Q and K ~ N(0, 3^2), V uniform[-1,1)."""
+    s = dict(SEEDS)
+    if seeds:
+        s.update(seeds)
+    shape = (batch, heads, seq_len, head_dim)
+    return fill_normal(shape, s["q"], 3.0), fill_normal(shape, s["k"], 3.0), fill_uniform(shape, s["v"])
+
+
 def make_uniform_inputs(batch: int, heads: int, seq_len: int, head_dim: int, seeds=None):
     """(q, k, v) uint16 bf16 bit arrays [B,H,N,D] of the uniform family."""
     s = dict(SEEDS)

@@ -121,14 +121,16 @@ def test_causal_work_layouts(fa, oracle_mod):
             check(oracle_mod, run_bits(fa, kernel, q, k, v, True), ref, f"causal layout {kernel} {(B, H, N, D)}")
 
 
-def growing_logit_inputs(oracle_mod, B, H, N, D, seed):
+def growing_logit_inputs(oracle_mod, B, H, N, D, seed, top=60.0):
     """Q ~ 0.5 + noise, K rows growing linearly along the sequence: every
-    query's logits rise key after key, to about +60 at the last key, so the
-    running max moves on (nearly) every 32-key tile and the fused kernels take
-    their base-move path over and over. `reverse` of the same data (largest
-    key first) never moves it."""
+    query's logits rise key after key, to about `top` at the last key. The
+    fused kernels move their exponent base when a tile's row sum passes 2^16,
+    and place it 48 log2 units above the row max, so a move follows about
+    every 64 log2 units (44 natural) of growth: `top` 60 moves it once or
+    twice per row, `top` 500 on every tile at N 256 and every third tile at N
+    1000. The same keys in falling order (largest first) never move it."""
     rng = np.random.default_rng(seed)
-    kappa = 120.0 / np.sqrt(D)  # scale * D * 0.5 * kappa = 60 at the last key
+    kappa = 2.0 * top / np.sqrt(D)  # scale * D * 0.5 * kappa = top at the last key
     ramp = kappa * np.arange(N, dtype=np.float64) / N
     q = 0.5 + 0.05 * rng.standard_normal((B, H, N, D))
     k = ramp[None, None, :, None] + 0.25 * rng.standard_normal((B, H, N, D))
@@ -137,14 +139,16 @@ def growing_logit_inputs(oracle_mod, B, H, N, D, seed):
 
 
 def test_base_moves(fa, oracle_mod):
-    """Inputs whose row max keeps growing (the exponent base moves on most
-    tiles), the same keys in falling order (it never moves after the first
-    tile), and N(0, 3^2) logits at a short length: all against the oracle,
-    dense and causal, both fused configurations, both head dims."""
+    """Inputs whose row max keeps growing (the exponent base moves once or
+    twice per row, or on most tiles for the steep ramp), the same keys in
+    falling order (it never moves after the first tile), and N(0, 3^2)
+    logits at a short length: all against the oracle, dense and causal,
+    every fused configuration, both head dims."""
     for D in (64, 128):
         for N in (256, 1000):
             q, k, v = growing_logit_inputs(oracle_mod, 1, 2, N, D, seed=N + D)
             cases = [("growing", q, k, v), ("falling", q, k[:, :, ::-1].copy(), v[:, :, ::-1].copy())]
+            cases.append(("steep",) + growing_logit_inputs(oracle_mod, 1, 2, N, D, seed=N + D + 1, top=500.0))
             cases.append(("stress",) + tuple(oracle_mod.make_inputs(1, 2, N, D, "stress")))
             for name, qq, kk, vv in cases:
                 for causal in (False, True):
