@@ -767,11 +767,13 @@ __global__ __launch_bounds__(64 * kGroups * kWpg) void fused_attention_kernel(co
         auto block_b = [&](auto par_tag, int jj) {
             constexpr int P = decltype(par_tag)::value;
             constexpr int B = P & 1;
-            // Head dim 128, dense: the wave of group 1 takes issue priority
-            // over its SIMD partner for this block. The SIMD otherwise
-            // favours the older group-0 wave, which then idles at the next
-            // barrier while group 1 finishes (measured 1% per launch).
-            constexpr bool kLeadB = G == 1 && D == 128 && !kCausal;
+            // Dense: the wave of group 1 takes issue priority over its SIMD
+            // partner for this block. The SIMD otherwise favours the older
+            // group-0 wave, which then idles at the next barrier while group
+            // 1 finishes (a per-step trace showed ~350 idle cycles per step
+            // at head_dim 64; measured 1% per launch at head_dim 128, 2% at
+            // 64).
+            constexpr bool kLeadB = G == 1 && !kCausal;
             if constexpr (kLeadB) __builtin_amdgcn_s_setprio(1);
             const bool rare = __any(tsum > kSumLimit);
             if (rare)
