@@ -17,8 +17,8 @@
 //   * Both GEMMs use v_mfma_f32_32x32x16_bf16. QK^T is computed transposed,
 //     S^T = K . Q^T (K tile = A operand, the wave's Q rows in registers = B
 //     operand): lane l then holds query l % 32 and keys 8*(r/4) + 4*(l/32) +
-//     r%4 of a 32-key tile, so a row's max and sum need one cross-lane step
-//     (v_permlane32_swap, or a shuffle for the final sum). PV is computed as O^T = V^T . P^T: the
+//     r%4 of a 32-key tile, so a row's max and its final sum need one
+//     cross-lane step (v_permlane32_swap). PV is computed as O^T = V^T . P^T: the
 //     exponentiated scores already are the B operand, P never leaves
 //     registers, and O^T's layout again gives lane l query l % 32, so the
 //     online-softmax rescale is per lane. The A operand (8 keys of one head
