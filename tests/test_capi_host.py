@@ -86,6 +86,9 @@ def test_argument_validation_before_launch(fa_lib):
     assert L.fa_launch_attention_unfused(fake, fake, fake, fake, fake, 1, 1, 64, 0, 0, None) == 1
     assert L.fa_launch_softmax_rows_inplace(None, 3, 10, None) == 1
     assert L.fa_launch_softmax_rows_inplace(fake, -1, 10, None) == 1
+    # one (batch, head) slab past 2^31 bytes: DMA offsets within a slab are 32-bit, so it is rejected
+    assert L.fa_launch_attention_tensorcore_v3(fake, fake, fake, fake, 1, 1, 1 << 24, 128, 0, None) == 1
+    assert L.fa_launch_attention_tensorcore_v3(fake, fake, fake, fake, 1, 1, 1 << 25, 64, 1, None) == 1
     # the pinned-configuration entry: only 0 (auto), 64 and 128 rows per workgroup
     for rows in (-1, 1, 32, 96, 512):
         assert L.fa_launch_attention_fused(fake, fake, fake, fake, 1, 1, 64, 64, 0, rows, None) == 1
