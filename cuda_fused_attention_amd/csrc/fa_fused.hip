@@ -407,12 +407,19 @@ __device__ __forceinline__ void exp_part(const f32x16& s, bf16x8& p, float m, fl
 // Per-element mask of a tile's scores: key offset of element r is
 // 8*(r/4) + 4*(lane/32) + r%4; `limit` = first dead key offset within the
 // tile for this lane's query, minus 4*(lane/32). Comparing the compile-time
-// part against `limit` keeps 16 key indices out of VGPRs.
+// part against `limit` keeps 16 key indices out of VGPRs. Written as a
+// select it compiles to one compare into VCC and one in-place v_cndmask per
+// element; the conditional-store form held the 16 compare results in SGPR
+// pairs and masked into fresh registers (about 30 more SGPRs and 8 more VGPRs
+// for the whole kernel, causal shapes 1-2 % slower).
 __device__ __forceinline__ void mask_tile(f32x16& s, int limit)
 {
 #pragma unroll
     for (int r = 0; r < 16; ++r)
-        if (8 * (r >> 2) + (r & 3) >= limit) s[r] = -INFINITY;
+    {
+        const float x = s[r];
+        s[r] = (8 * (r >> 2) + (r & 3) < limit) ? x : -INFINITY;
+    }
 }
 
 // Both lane halves' values of a row: v_permlane32_swap of two copies of x
