@@ -10,9 +10,12 @@ headline workload is BASELINE config 2, (2,8,2048,64) dense; the other three
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
 
-Prints ONE JSON line. Order: the per-shape extras (median/IQR of 5 warmups +
-30 individually timed launches per kernel, benchmarks/bench_flash_attention.cu:265-299,
-for the four (2,8,2048,D) cases and the v0 baseline), then a clock ramp
+Prints ONE JSON line. Order: the per-shape extras for the four (2,8,2048,D)
+cases (median/IQR of 5 warmups + 30 individually timed launches per kernel,
+benchmarks/bench_flash_attention.cu:265-299; then, after a clock ramp, the
+average of back-to-back launches between one event pair for v3 and v0, with
+the fraction of peak and the speed-up over v0 under both timings; and the v0
+per-stage medians, benchmarks/profile_attention_v0.cu:141-190), then a clock ramp
 (untimed launches of the measured kernel for --ramp-s seconds: the GPU's
 clock takes a few hundred milliseconds of load to settle, and a cold start
 reads up to 10 % slow), then W untimed warmup launches, a synchronisation, and
@@ -26,6 +29,7 @@ loads the oracle.
 from __future__ import annotations
 
 import argparse
+import hashlib
 import json
 import os
 import sys
@@ -51,6 +55,19 @@ FAMILY = {"c5": "stress"}
 # (2,8,2048,D) shapes.
 EXTRA_WORKLOADS = ("c2", "c2_causal", "headline", "c3")
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
+# The sources that define the fused kernel's code: profiles/traffic.json
+# records their hash next to each counter measurement, and a measurement
+# taken on other sources is reported as stale (traffic null).
+KERNEL_SOURCES = ("cuda_fused_attention_amd/csrc/fa_fused.hip", "cuda_fused_attention_amd/csrc/fa_fused_schedule.hpp",
+                  "cuda_fused_attention_amd/csrc/fa_common.hpp", "cuda_fused_attention_amd/_build.py")
+
+
+def kernel_source_sha() -> str:
+    h = hashlib.sha256()
+    for rel in KERNEL_SOURCES:
+        with open(os.path.join(ROOT, rel), "rb") as fh:
+            h.update(rel.encode() + b"\0" + fh.read() + b"\0")
+    return h.hexdigest()[:16]
 
 
 def baseline_flops(B, H, N, D, causal):
@@ -189,14 +206,61 @@ def cpu_baseline_sampled(host_inputs, B, H, N, D, causal, threads, flops):
 
 
 def load_traffic(key):
+    """(HBM bytes per launch, status) from profiles/traffic.json for this
+    kernel:workload; None unless it was measured on the current kernel sources."""
     try:
         with open(TRAFFIC_FILE) as fh:
             entry = json.load(fh).get(key)
     except (OSError, ValueError):
-        return None
+        return None, "no traffic.json"
     if not entry:
-        return None
-    return entry.get("hbm_bytes_per_launch")
+        return None, f"no measurement for {key}"
+    if entry.get("kernel_source_sha") != kernel_source_sha():
+        return None, "stale: measured on other kernel sources"
+    return entry.get("hbm_bytes_per_launch"), f"rocprofv3 FETCH_SIZE/WRITE_SIZE, {entry.get('source')}"
+
+
+def measure_back_to_back(fa, dev, B, H, N, D, causal, kernel, ws=None, min_s=0.15, ramp_s=0.2):
+    """Average launch time (ms) of back-to-back launches between one event
+    pair (fa_time_batch), after `ramp_s` seconds of untimed launches, over
+    enough launches for about `min_s` seconds."""
+    import torch
+
+    shape = fa.AttentionShape(B, H, N, D)
+    o = torch.empty_like(dev[0])
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < ramp_s:
+        fa.time_batch(kernel, *dev, o, ws, shape, causal, iters=20)
+    probe = fa.time_batch(kernel, *dev, o, ws, shape, causal, iters=20) / 20
+    iters = max(20, int(min_s * 1e3 / max(probe, 1e-3)))
+    return fa.time_batch(kernel, *dev, o, ws, shape, causal, iters=iters) / iters, iters
+
+
+def v0_stage_timing(fa, dev, B, H, N, D, causal, iters=30, warmup=5):
+    """benchmarks/profile_attention_v0.cu:141-190: per-stage milliseconds of
+    the instrumented v0 launch (QK, softmax, PV and total), median and IQR
+    over `iters` launches, each synchronised."""
+    import torch
+
+    shape = fa.AttentionShape(B, H, N, D)
+    ws = torch.empty(fa.unfused_workspace_bytes(shape) // 4, dtype=torch.float32, device="cuda")
+    o = torch.empty_like(dev[0])
+    events = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+    samples = {"qk": [], "softmax": [], "pv": [], "total": []}
+    for it in range(warmup + iters):
+        fa.launch_attention_unfused_profile(*dev, o, ws, shape, causal, events=events)
+        torch.cuda.synchronize()
+        if it < warmup:
+            continue
+        t = [events[i].elapsed_time(events[i + 1]) for i in range(3)]
+        for name, val in zip(("qk", "softmax", "pv"), t):
+            samples[name].append(val)
+        samples["total"].append(events[0].elapsed_time(events[3]))
+    out = {"shape": [B, H, N, D], "causal": causal, "timed_iters": iters}
+    for name, xs in samples.items():
+        summ = fa.summarize(xs)
+        out[name] = {"median_ms": summ["median_ms"], "iqr_ms": summ["iqr_ms"]}
+    return out
 
 
 def main():
@@ -260,9 +324,27 @@ def main():
             v0["algorithmic_bytes"] = v0_bytes
             v0["reference_model_bytes"] = 20.0 * b * h * n * n + 8.0 * b * h * n * d
             entry["v0_unfused"] = v0
+            entry["v3_rows_per_block"] = fa.tensorcore_v3_rows_per_block(sh, c)
+            # Back-to-back: the kernel's own duration, without the ~7 us of
+            # idle-queue dispatch each individually timed launch carries.
+            flops_s = baseline_flops(b, h, n, d, c)
+            b2b_ms, b2b_iters = measure_back_to_back(fa, sdev, b, h, n, d, c, "v3_mfma")
+            entry["v3_mfma"].update({"b2b_ms": b2b_ms, "b2b_launches": b2b_iters,
+                                     "b2b_tflops": flops_s / (b2b_ms * 1e-3) / 1e12,
+                                     "b2b_frac": flops_s / (b2b_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS})
+            v0_b2b_ms, v0_iters = measure_back_to_back(fa, sdev, b, h, n, d, c, "v0_unfused", ws, min_s=0.1,
+                                                       ramp_s=0.05)
+            v0.update({"b2b_ms": v0_b2b_ms, "b2b_launches": v0_iters,
+                       "b2b_hbm_gbps": v0_bytes / (v0_b2b_ms * 1e-3) / 1e9})
             entry["speedup_vs_v0"] = v0["median_ms"] / entry["v3_mfma"]["median_ms"]
+            entry["speedup_vs_v0_b2b"] = v0_b2b_ms / b2b_ms
             shapes[name] = entry
             del ws, sdev
+        # v0 per-stage record at the reference's profiling shape (c2)
+        b, h, n, d, c = WORKLOADS["c2"]
+        _, sdev = make_device_inputs(b, h, n, d)
+        v0_stages = v0_stage_timing(fa, sdev, b, h, n, d, c)
+        del sdev
         torch.cuda.synchronize()
 
     # Clock ramp: untimed launches until --ramp-s seconds have passed.
@@ -291,6 +373,7 @@ def main():
         torch.neg(x, out=y)
         torch.cuda.synchronize()
 
+    traffic, traffic_source = load_traffic(f"{args.kernel}:{args.workload}")
     result = {
         "metric": METRIC,
         "value": round(value, 3),
@@ -318,7 +401,8 @@ def main():
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_BF16_TFLOPS, 5),
-            "traffic": load_traffic(f"{args.kernel}:{args.workload}"),
+            "traffic": traffic,
+            "traffic_source": traffic_source,
             "avg_launch_us": avg_launch_ms * 1e3,
             "algorithmic_flops_per_launch": flops,
             "min_hbm_bytes_per_launch": 8.0 * B * H * N * D,
@@ -338,6 +422,7 @@ def main():
     result["clock_ramp_launches"] = ramp_launches
     if shapes is not None:
         result["shapes"] = shapes
+        result["v0_stages"] = v0_stages
         if args.workload in shapes:
             result["v0"] = {"bound": "hbm", "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                             "achieved": shapes[args.workload]["v0_unfused"]["hbm_gbps"],

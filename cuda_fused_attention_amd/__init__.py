@@ -76,6 +76,8 @@ class TilingInfo(ctypes.Structure):
 _vp = ctypes.c_void_p
 _i = ctypes.c_int
 _SIGNATURES = {
+    "fa_get_last_error": (_i, []),
+    "fa_peek_at_last_error": (_i, []),
     "fa_default_scale": (ctypes.c_float, [_i]),
     "fa_attention_flops": (ctypes.c_double, [_i, _i, _i, _i, _i]),
     "fa_unfused_workspace_bytes": (ctypes.c_size_t, [_i, _i, _i, _i]),
@@ -86,6 +88,7 @@ _SIGNATURES = {
     "fa_launch_attention_tensorcore_v3": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp]),
     "fa_launch_attention_fused": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp]),
     "fa_query_fused": (_i, [_i, _i, ctypes.POINTER(TilingInfo)]),
+    "fa_tensorcore_v3_rows_per_block": (_i, [_i, _i, _i, _i, _i]),
     "fa_query_tensorcore_v3": (_i, [_i, ctypes.POINTER(TilingInfo)]),
     "fa_tensorcore_v3_hbm_bytes": (ctypes.c_double, [_i, _i, _i, _i, _i]),
     "fa_tensorcore_v3b_supported": (_i, [_i]),
@@ -207,6 +210,21 @@ def tensorcore_v3_hbm_bytes(shape, causal: bool) -> float:
 def tensorcore_v3b_hbm_bytes(shape, causal: bool) -> float:
     s = _shape_of(shape)
     return float(lib().fa_tensorcore_v3b_hbm_bytes(s.batch, s.heads, s.seq_len, s.head_dim, int(causal)))
+
+
+def tensorcore_v3_rows_per_block(shape, causal: bool) -> int:
+    """Query rows per workgroup the v3 entry runs at this shape (64, 128 or 256)."""
+    s = _shape_of(shape)
+    return int(lib().fa_tensorcore_v3_rows_per_block(s.batch, s.heads, s.seq_len, s.head_dim, int(causal)))
+
+
+def get_last_error() -> int:
+    """The calling thread's last non-zero C-ABI status (reset to 0)."""
+    return int(lib().fa_get_last_error())
+
+
+def peek_at_last_error() -> int:
+    return int(lib().fa_peek_at_last_error())
 
 
 def build_info() -> str:

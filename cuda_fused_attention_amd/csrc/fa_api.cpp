@@ -10,8 +10,31 @@
 #include "../../include/fa_mi355x.h"
 #include "../../include/flash_attention.h"
 #include "../../include/flash_attention_v0_profile.h"
+#include "fa_common.hpp"
+
+namespace {
+
+// The calling thread's last non-success status of a C-ABI call
+// (fa_get_last_error / fa_peek_at_last_error; hipGetLastError semantics).
+thread_local int t_last_status = 0;
+
+}  // namespace
+
+namespace fa {
+
+int record_status(int status)
+{
+    if (status != 0 && status != FA_ERROR_UNSUPPORTED) t_last_status = status;
+    return status;
+}
+
+}  // namespace fa
 
 namespace cuda_op_lab::flash_attention {
+
+hipError_t get_last_error() { return static_cast<hipError_t>(fa_get_last_error()); }
+
+hipError_t peek_at_last_error() { return static_cast<hipError_t>(fa_peek_at_last_error()); }
 
 namespace {
 
@@ -32,6 +55,9 @@ FusedTilingInfo to_cpp(const fa_tiling_info& c)
 }
 
 }  // namespace
+
+// The launchers return void, as the reference's do; a non-zero status of
+// the C-ABI call under them is kept per thread for get_last_error().
 
 double attention_flops(const AttentionShape& s, bool causal)
 {
@@ -178,9 +204,20 @@ struct EventPair
 
 extern "C" {
 
-int fa_time_launches(int which, const void* q, const void* k, const void* v, void* o, float* workspace, int batch,
-                     int heads, int seq_len, int head_dim, int causal, int warmup, int iters, float* samples_ms,
-                     void* stream)
+int fa_get_last_error(void)
+{
+    const int status = t_last_status;
+    t_last_status = 0;
+    return status;
+}
+
+int fa_peek_at_last_error(void) { return t_last_status; }
+
+namespace {
+
+int time_launches(int which, const void* q, const void* k, const void* v, void* o, float* workspace, int batch,
+                  int heads, int seq_len, int head_dim, int causal, int warmup, int iters, float* samples_ms,
+                  void* stream)
 {
     if (warmup < 0 || iters <= 0 || !samples_ms) return hipErrorInvalidValue;
     hipStream_t s = static_cast<hipStream_t>(stream);
@@ -210,8 +247,8 @@ int fa_time_launches(int which, const void* q, const void* k, const void* v, voi
     return hipSuccess;
 }
 
-int fa_time_batch(int which, const void* q, const void* k, const void* v, void* o, float* workspace, int batch,
-                  int heads, int seq_len, int head_dim, int causal, int iters, float* total_ms, void* stream)
+int time_batch(int which, const void* q, const void* k, const void* v, void* o, float* workspace, int batch,
+               int heads, int seq_len, int head_dim, int causal, int iters, float* total_ms, void* stream)
 {
     if (iters <= 0 || !total_ms) return hipErrorInvalidValue;
     hipStream_t s = static_cast<hipStream_t>(stream);
@@ -232,6 +269,23 @@ int fa_time_batch(int which, const void* q, const void* k, const void* v, void* 
     if (!std::isfinite(ms) || ms <= 0.0f) return hipErrorInvalidValue;
     *total_ms = ms;
     return hipSuccess;
+}
+
+}  // namespace
+
+int fa_time_launches(int which, const void* q, const void* k, const void* v, void* o, float* workspace, int batch,
+                     int heads, int seq_len, int head_dim, int causal, int warmup, int iters, float* samples_ms,
+                     void* stream)
+{
+    return fa::record_status(time_launches(which, q, k, v, o, workspace, batch, heads, seq_len, head_dim, causal,
+                                           warmup, iters, samples_ms, stream));
+}
+
+int fa_time_batch(int which, const void* q, const void* k, const void* v, void* o, float* workspace, int batch,
+                  int heads, int seq_len, int head_dim, int causal, int iters, float* total_ms, void* stream)
+{
+    return fa::record_status(time_batch(which, q, k, v, o, workspace, batch, heads, seq_len, head_dim, causal, iters,
+                                        total_ms, stream));
 }
 
 const char* fa_build_info(void)

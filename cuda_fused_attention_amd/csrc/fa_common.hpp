@@ -5,8 +5,37 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <tuple>
+#include <type_traits>
+#include <utility>
 
 namespace fa {
+
+// Launches `kernel` on `stream` through hipLaunchKernel and returns the
+// runtime's status for this launch alone (no hipGetLastError, so an earlier,
+// unrelated error is neither reported here nor cleared; a failed launch
+// stays in HIP's own last-error state as well, where a caller's
+// hipGetLastError finds it). Arguments are converted to the kernel's
+// parameter types first.
+template <typename... Params, typename... Args>
+hipError_t launch_kernel(void (*kernel)(Params...), dim3 grid, dim3 block, hipStream_t stream, Args&&... args)
+{
+    static_assert(sizeof...(Params) == sizeof...(Args) && sizeof...(Params) > 0, "kernel argument count");
+    std::tuple<std::decay_t<Params>...> values{static_cast<std::decay_t<Params>>(std::forward<Args>(args))...};
+    return std::apply(
+        [&](auto&... v) {
+            void* ptrs[] = {static_cast<void*>(&v)...};
+            return hipLaunchKernel(reinterpret_cast<const void*>(kernel), grid, block, ptrs, 0, stream);
+        },
+        values);
+}
+
+// Records a non-success status of a C-ABI call in the calling thread's
+// last-error slot (read by fa_get_last_error / fa_peek_at_last_error) and
+// returns it unchanged. FA_ERROR_UNSUPPORTED (an unsupported head_dim, which
+// the reference's launchers skip silently) is not recorded. Defined in
+// fa_api.cpp.
+int record_status(int status);
 
 // bf16 is carried as raw 16-bit patterns in memory (uint16_t); conversions
 // below are exact (bf16 -> f32) or IEEE round-to-nearest-even (f32 -> bf16,

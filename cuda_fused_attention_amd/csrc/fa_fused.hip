@@ -79,6 +79,7 @@
 
 #include "fa_common.hpp"
 #include "fa_fused_schedule.hpp"
+#include "fa_resources.hpp"
 #include "../../include/fa_mi355x.h"
 
 namespace {
@@ -988,12 +989,12 @@ const void* pick_kernel(int head_dim, bool causal)
 }
 
 template <int D, int kWpg, bool kCausal, int kGroups>
-void launch_typed(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o, int n, int q_blocks,
-                  int total, float c_log2, int paired, hipStream_t stream)
+hipError_t launch_typed(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o, int n, int q_blocks,
+                        int total, float c_log2, int paired, hipStream_t stream)
 {
-    hipLaunchKernelGGL((fused_attention_kernel<D, kWpg, kCausal, kGroups>), dim3(static_cast<unsigned>(total)),
-                       dim3(Cfg<D, kWpg, kGroups>::kThreads), 0, stream, q, k, v, o, n, q_blocks, total, c_log2,
-                       paired);
+    return fa::launch_kernel(fused_attention_kernel<D, kWpg, kCausal, kGroups>, dim3(static_cast<unsigned>(total)),
+                             dim3(Cfg<D, kWpg, kGroups>::kThreads), stream, q, k, v, o, n, q_blocks, total, c_log2,
+                             paired);
 }
 
 // Compute units of the current device (cached per device; 256 on an
@@ -1050,16 +1051,10 @@ int launch_fused(const void* q, const void* k, const void* v, void* o, int batch
     const int qbk = static_cast<int>(q_blocks);
     const int tot = static_cast<int>(total);
     if (head_dim == 64)
-    {
-        if (causal) launch_typed<64, kWpg, true, kGroups>(qb, kb, vb, ob, seq_len, qbk, tot, c_log2, paired, stream);
-        else launch_typed<64, kWpg, false, kGroups>(qb, kb, vb, ob, seq_len, qbk, tot, c_log2, 0, stream);
-    }
-    else
-    {
-        if (causal) launch_typed<128, kWpg, true, kGroups>(qb, kb, vb, ob, seq_len, qbk, tot, c_log2, paired, stream);
-        else launch_typed<128, kWpg, false, kGroups>(qb, kb, vb, ob, seq_len, qbk, tot, c_log2, 0, stream);
-    }
-    return static_cast<int>(hipGetLastError());
+        return causal ? launch_typed<64, kWpg, true, kGroups>(qb, kb, vb, ob, seq_len, qbk, tot, c_log2, paired, stream)
+                      : launch_typed<64, kWpg, false, kGroups>(qb, kb, vb, ob, seq_len, qbk, tot, c_log2, 0, stream);
+    return causal ? launch_typed<128, kWpg, true, kGroups>(qb, kb, vb, ob, seq_len, qbk, tot, c_log2, paired, stream)
+                  : launch_typed<128, kWpg, false, kGroups>(qb, kb, vb, ob, seq_len, qbk, tot, c_log2, 0, stream);
 }
 
 // Rows per workgroup the v3 entry point uses for a shape (measured on
@@ -1122,9 +1117,16 @@ int query_fused(int head_dim, fa_tiling_info* info)
     int cus = 0;
     if ((e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device)) != hipSuccess) return e;
     info->compute_units = cus;
-    // hipFuncAttributes reports one register count (numRegs); AGPR use is
-    // visible in the compiler's resource remarks, not through this API.
-    info->agprs_per_thread = 0;
+    // hipFuncAttributes reports one register count (numRegs); the AGPR count
+    // comes from the compiler's resource report of this kernel, recorded in
+    // a table when the library is built (-1 if the build had none).
+    info->agprs_per_thread = -1;
+    for (int x = 0; x < fa::kFusedKernelResourceCount; ++x)
+    {
+        const fa::KernelResources& r = fa::kFusedKernelResources[x];
+        if (r.head_dim == head_dim && r.waves_per_group == kWpg && r.groups == kGroups && r.causal == 0)
+            info->agprs_per_thread = r.agprs;
+    }
     return hipSuccess;
 }
 
@@ -1154,15 +1156,22 @@ extern "C" {
 
 int fa_tensorcore_v3_supported(int head_dim) { return head_dim == 64 || head_dim == 128; }
 
+int fa_tensorcore_v3_rows_per_block(int batch, int heads, int seq_len, int head_dim, int causal)
+{
+    if (head_dim != 64 && head_dim != 128) return 0;
+    return auto_rows_per_block(batch, heads, seq_len, causal);
+}
+
 int fa_launch_attention_fused(const void* q, const void* k, const void* v, void* o, int batch, int heads,
                               int seq_len, int head_dim, int causal, int rows_per_block, void* stream)
 {
     if (rows_per_block == 0) rows_per_block = auto_rows_per_block(batch, heads, seq_len, causal);
-    if (rows_per_block == 128) return launch_fused<4>(q, k, v, o, batch, heads, seq_len, head_dim, causal, stream);
-    if (rows_per_block == 64) return launch_fused<2>(q, k, v, o, batch, heads, seq_len, head_dim, causal, stream);
-    if (rows_per_block == 256)
-        return launch_fused<8, 1>(q, k, v, o, batch, heads, seq_len, head_dim, causal, stream);
-    return hipErrorInvalidValue;
+    int status = hipErrorInvalidValue;
+    if (rows_per_block == 128) status = launch_fused<4>(q, k, v, o, batch, heads, seq_len, head_dim, causal, stream);
+    else if (rows_per_block == 64) status = launch_fused<2>(q, k, v, o, batch, heads, seq_len, head_dim, causal, stream);
+    else if (rows_per_block == 256)
+        status = launch_fused<8, 1>(q, k, v, o, batch, heads, seq_len, head_dim, causal, stream);
+    return fa::record_status(status);
 }
 
 int fa_launch_attention_tensorcore_v3(const void* q, const void* k, const void* v, void* o, int batch, int heads,
@@ -1171,19 +1180,23 @@ int fa_launch_attention_tensorcore_v3(const void* q, const void* k, const void* 
     return fa_launch_attention_fused(q, k, v, o, batch, heads, seq_len, head_dim, causal, 0, stream);
 }
 
-int fa_query_tensorcore_v3(int head_dim, fa_tiling_info* info) { return query_fused<4>(head_dim, info); }
+int fa_query_tensorcore_v3(int head_dim, fa_tiling_info* info) { return fa::record_status(query_fused<4>(head_dim, info)); }
 
 int fa_query_fused(int head_dim, int rows_per_block, fa_tiling_info* info)
 {
-    if (rows_per_block == 128) return query_fused<4>(head_dim, info);
-    if (rows_per_block == 64) return query_fused<2>(head_dim, info);
-    if (rows_per_block == 256) return query_fused<8, 1>(head_dim, info);
-    return hipErrorInvalidValue;
+    int status = hipErrorInvalidValue;
+    if (rows_per_block == 128) status = query_fused<4>(head_dim, info);
+    else if (rows_per_block == 64) status = query_fused<2>(head_dim, info);
+    else if (rows_per_block == 256) status = query_fused<8, 1>(head_dim, info);
+    return fa::record_status(status);
 }
 
+// The model for the configuration the v3 entry runs at this shape (64, 128
+// or 256 query rows per workgroup; 32-key tiles).
 double fa_tensorcore_v3_hbm_bytes(int batch, int heads, int seq_len, int head_dim, int causal)
 {
-    return blocked_hbm_bytes(batch, heads, seq_len, head_dim, causal, 128);
+    return blocked_hbm_bytes(batch, heads, seq_len, head_dim, causal,
+                             auto_rows_per_block(batch, heads, seq_len, causal));
 }
 
 int fa_tensorcore_v3b_supported(int head_dim) { return head_dim == 64 || head_dim == 128; }
@@ -1191,10 +1204,10 @@ int fa_tensorcore_v3b_supported(int head_dim) { return head_dim == 64 || head_di
 int fa_launch_attention_tensorcore_v3b(const void* q, const void* k, const void* v, void* o, int batch, int heads,
                                        int seq_len, int head_dim, int causal, void* stream)
 {
-    return launch_fused<2>(q, k, v, o, batch, heads, seq_len, head_dim, causal, stream);
+    return fa::record_status(launch_fused<2>(q, k, v, o, batch, heads, seq_len, head_dim, causal, stream));
 }
 
-int fa_query_tensorcore_v3b(int head_dim, fa_tiling_info* info) { return query_fused<2>(head_dim, info); }
+int fa_query_tensorcore_v3b(int head_dim, fa_tiling_info* info) { return fa::record_status(query_fused<2>(head_dim, info)); }
 
 double fa_tensorcore_v3b_hbm_bytes(int batch, int heads, int seq_len, int head_dim, int causal)
 {

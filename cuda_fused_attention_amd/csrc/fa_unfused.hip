@@ -355,18 +355,13 @@ constexpr int kMaxGridY = 65535;
 int launch_softmax(float* s, int rows, int cols, hipStream_t stream)
 {
     const dim3 grid(static_cast<unsigned>(rows));
+    const dim3 block(kThreads);
     const bool vec = (cols % 4 == 0) && aligned16(s);
-    if (vec && cols <= 1024 * 1)
-        hipLaunchKernelGGL(v0_softmax_rows_reg_kernel<1>, grid, dim3(kThreads), 0, stream, s, cols);
-    else if (vec && cols <= 1024 * 2)
-        hipLaunchKernelGGL(v0_softmax_rows_reg_kernel<2>, grid, dim3(kThreads), 0, stream, s, cols);
-    else if (vec && cols <= 1024 * 4)
-        hipLaunchKernelGGL(v0_softmax_rows_reg_kernel<4>, grid, dim3(kThreads), 0, stream, s, cols);
-    else if (vec && cols <= 1024 * 8)
-        hipLaunchKernelGGL(v0_softmax_rows_reg_kernel<8>, grid, dim3(kThreads), 0, stream, s, cols);
-    else
-        hipLaunchKernelGGL(v0_softmax_rows_loop_kernel, grid, dim3(kThreads), 0, stream, s, cols);
-    return static_cast<int>(hipGetLastError());
+    if (vec && cols <= 1024 * 1) return fa::launch_kernel(v0_softmax_rows_reg_kernel<1>, grid, block, stream, s, cols);
+    if (vec && cols <= 1024 * 2) return fa::launch_kernel(v0_softmax_rows_reg_kernel<2>, grid, block, stream, s, cols);
+    if (vec && cols <= 1024 * 4) return fa::launch_kernel(v0_softmax_rows_reg_kernel<4>, grid, block, stream, s, cols);
+    if (vec && cols <= 1024 * 8) return fa::launch_kernel(v0_softmax_rows_reg_kernel<8>, grid, block, stream, s, cols);
+    return fa::launch_kernel(v0_softmax_rows_loop_kernel, grid, block, stream, s, cols);
 }
 
 int validate_unfused(const void* q, const void* k, const void* v, void* o, const float* workspace,
@@ -409,13 +404,8 @@ int launch_unfused_impl(const void* q, const void* k, const void* v, void* o, fl
     }
     const bool vec_qk = (d % 8 == 0) && aligned16(q) && aligned16(k);
     const dim3 grid_s(static_cast<unsigned>(tiles_n * tiles_n), static_cast<unsigned>(bh));
-    if (vec_qk)
-        hipLaunchKernelGGL(v0_scores_kernel<true>, grid_s, dim3(kThreads), 0, stream, qb, kb, workspace, n, d,
-                           tiles_n, scale, causal);
-    else
-        hipLaunchKernelGGL(v0_scores_kernel<false>, grid_s, dim3(kThreads), 0, stream, qb, kb, workspace, n, d,
-                           tiles_n, scale, causal);
-    hipError_t e = hipGetLastError();
+    hipError_t e = fa::launch_kernel(vec_qk ? v0_scores_kernel<true> : v0_scores_kernel<false>, grid_s,
+                                     dim3(kThreads), stream, qb, kb, workspace, n, d, tiles_n, scale, causal);
     if (e != hipSuccess) return e;
     if (events && (e = hipEventRecord(events[1], stream)) != hipSuccess) return e;
 
@@ -426,11 +416,8 @@ int launch_unfused_impl(const void* q, const void* k, const void* v, void* o, fl
 
     const bool vec_pv = (n % 8 == 0) && (d % 8 == 0) && aligned16(workspace) && aligned16(v) && aligned16(o);
     const dim3 grid_o(static_cast<unsigned>(tiles_n * tiles_d), static_cast<unsigned>(bh));
-    if (vec_pv)
-        hipLaunchKernelGGL(v0_pv_kernel<true>, grid_o, dim3(kThreads), 0, stream, workspace, vb, ob, n, d, tiles_d);
-    else
-        hipLaunchKernelGGL(v0_pv_kernel<false>, grid_o, dim3(kThreads), 0, stream, workspace, vb, ob, n, d, tiles_d);
-    e = hipGetLastError();
+    e = fa::launch_kernel(vec_pv ? v0_pv_kernel<true> : v0_pv_kernel<false>, grid_o, dim3(kThreads), stream,
+                          workspace, vb, ob, n, d, tiles_d);
     if (e != hipSuccess) return e;
     if (events && (e = hipEventRecord(events[3], stream)) != hipSuccess) return e;
     return hipSuccess;
@@ -457,25 +444,26 @@ size_t fa_unfused_workspace_bytes(int batch, int heads, int seq_len, int /*head_
 
 int fa_launch_softmax_rows_inplace(float* s, int rows, int cols, void* stream)
 {
-    if (rows < 0 || cols < 0) return hipErrorInvalidValue;
+    if (rows < 0 || cols < 0) return fa::record_status(hipErrorInvalidValue);
     if (rows == 0 || cols == 0) return hipSuccess;
-    if (!s) return hipErrorInvalidValue;
-    return launch_softmax(s, rows, cols, static_cast<hipStream_t>(stream));
+    if (!s) return fa::record_status(hipErrorInvalidValue);
+    return fa::record_status(launch_softmax(s, rows, cols, static_cast<hipStream_t>(stream)));
 }
 
 int fa_launch_attention_unfused(const void* q, const void* k, const void* v, void* o, float* workspace,
                                 int batch, int heads, int seq_len, int head_dim, int causal, void* stream)
 {
-    return launch_unfused_impl(q, k, v, o, workspace, batch, heads, seq_len, head_dim, causal, nullptr,
-                               static_cast<hipStream_t>(stream));
+    return fa::record_status(launch_unfused_impl(q, k, v, o, workspace, batch, heads, seq_len, head_dim, causal,
+                                                 nullptr, static_cast<hipStream_t>(stream)));
 }
 
 int fa_launch_attention_unfused_profile(const void* q, const void* k, const void* v, void* o, float* workspace,
                                         int batch, int heads, int seq_len, int head_dim, int causal,
                                         void* const* events, void* stream)
 {
-    return launch_unfused_impl(q, k, v, o, workspace, batch, heads, seq_len, head_dim, causal,
-                               reinterpret_cast<hipEvent_t const*>(events), static_cast<hipStream_t>(stream));
+    return fa::record_status(launch_unfused_impl(q, k, v, o, workspace, batch, heads, seq_len, head_dim, causal,
+                                                 reinterpret_cast<hipEvent_t const*>(events),
+                                                 static_cast<hipStream_t>(stream)));
 }
 
 }  // extern "C"

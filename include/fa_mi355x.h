@@ -20,8 +20,16 @@
  *                          launched (the reference's launchers return silently
  *                          here, kernels/v3/v3_tensorcore.cu:743-744);
  *   hipErrorInvalidValue   null pointer with a non-empty shape, negative
- *                          dimension, or a shape beyond the grid limits;
+ *                          dimension, misaligned fused-kernel base, a slab
+ *                          past 2^31 bytes, or a shape beyond the grid limits
+ *                          (host-side rejections: nothing is launched);
+ *   a hipError_t           the runtime refused a kernel launch (the status of
+ *                          that launch alone; it also stays in HIP's own
+ *                          last-error state, so hipGetLastError sees it);
  *   0 with no launch       any of batch, heads, seq_len equal to 0.
+ * Every non-zero status except FA_ERROR_UNSUPPORTED is also kept per thread
+ * for fa_get_last_error / fa_peek_at_last_error, which is how a caller of the
+ * void C++ launchers of flash_attention.h sees host-side rejections.
  *
  * Reference interface each symbol replaces is cited per declaration
  * (paths relative to the RichterWang/cuda_fused_attention tree).
@@ -52,10 +60,20 @@ typedef struct fa_tiling_info {
     int max_blocks_per_sm;           /* workgroups resident per CU */
     int device_shared_bytes_per_sm;  /* LDS per CU */
     int shared_limited_blocks_per_sm;
-    int agprs_per_thread;            /* accumulation VGPRs (MI355X) */
+    int agprs_per_thread;            /* accumulation VGPRs (MI355X), from the
+                                        compiler's report; -1 if unknown */
     int waves_per_block;             /* wave64 count per workgroup (MI355X) */
     int compute_units;               /* CUs on the current device (MI355X) */
 } fa_tiling_info;
+
+/* No counterpart in the reference (its launchers return void and leave
+ * errors to cudaGetLastError): the calling thread's last non-zero status of
+ * an fa_* launcher, query or timing call, FA_ERROR_UNSUPPORTED excepted.
+ * fa_get_last_error returns it and resets it to 0 (hipGetLastError
+ * semantics); fa_peek_at_last_error leaves it. For callers of the void C++
+ * launchers, whose host-side rejections never reach HIP's error state. */
+int fa_get_last_error(void);
+int fa_peek_at_last_error(void);
 
 /* include/flash_attention.h:21-24 — 1.0f / sqrtf(head_dim). */
 float fa_default_scale(int head_dim);
@@ -115,16 +133,26 @@ int fa_launch_attention_fused(const void* q, const void* k, const void* v, void*
 
 /* No counterpart in the reference: fa_query_tensorcore_v3 for the
  * configuration fa_launch_attention_fused runs with rows_per_block (64, 128
- * or 256). */
+ * or 256). agprs_per_thread comes from the compiler's resource report of
+ * the kernel, recorded when the library was built. */
 int fa_query_fused(int head_dim, int rows_per_block, fa_tiling_info* info);
 
-/* include/flash_attention.h:94, kernels/v3/v3_tensorcore.cu:752-790 */
+/* No counterpart in the reference (whose v3 has one configuration): the
+ * query rows per workgroup (64, 128 or 256) fa_launch_attention_tensorcore_v3
+ * runs at this shape on the current device; 0 for an unsupported head_dim. */
+int fa_tensorcore_v3_rows_per_block(int batch, int heads, int seq_len, int head_dim, int causal);
+
+/* include/flash_attention.h:94, kernels/v3/v3_tensorcore.cu:752-790 — the
+ * 128-row (two wave group) configuration, the one the reference's
+ * single-configuration query corresponds to; fa_query_fused reports the
+ * others and fa_tensorcore_v3_rows_per_block says which one a shape runs. */
 int fa_query_tensorcore_v3(int head_dim, fa_tiling_info* info);
 
 /* include/flash_attention.h:96, kernels/v3/v3_tensorcore.cu:795-818 — the
- * algorithmic HBM model of the fused kernel: Q read and O written once, K/V
- * tiles counted once per query block that loads them (an upper bound; L2
- * reuse brings the measured figure to Q+K+V+O once). */
+ * algorithmic HBM model of the fused kernel in the configuration the v3
+ * entry runs at this shape: Q read and O written once, K/V tiles counted
+ * once per query block that loads them (an upper bound; L2 reuse brings the
+ * measured figure to Q+K+V+O once). */
 double fa_tensorcore_v3_hbm_bytes(int batch, int heads, int seq_len, int head_dim, int causal);
 
 /* include/flash_attention.h:101-107 — the reference's v3b occupancy variant.

@@ -10,6 +10,11 @@
 //     through hipGetLastError / the next synchronisation;
 //   * an unsupported head_dim launches nothing and returns silently;
 //   * callers own every buffer; launchers allocate nothing.
+// Added: a launch this library rejects on the host (misaligned fused-kernel
+// base, a slab past 2^31 bytes, a grid beyond the device limits, a null
+// pointer) launches nothing and never reaches HIP's error state; it is
+// reported by get_last_error() / peek_at_last_error() below, which also see
+// every launch the runtime refused.
 // The kernels behind these calls are the gfx950 ones of fa_mi355x.h; the
 // reference's v1 (fused_row) and v2 (fusedtiling, v2b) study kernels are not
 // rebuilt: their queries report supported = false and their launchers are
@@ -32,6 +37,14 @@ struct AttentionShape
     int seq_len;   // query and key/value length
     int head_dim;  // 64 or 128 for the fused kernels; any for v0
 };
+
+// No counterpart in the reference: the calling thread's last error of a
+// launcher or query of this library (host-side rejections and refused
+// launches; an unsupported head_dim is silent). get_last_error() returns it
+// and resets it to hipSuccess, like hipGetLastError; peek_at_last_error()
+// leaves it.
+hipError_t get_last_error();
+hipError_t peek_at_last_error();
 
 inline float default_scale(int head_dim)
 {

@@ -108,6 +108,8 @@ def lib():
         L.fa_oracle_mt19937_10000th.argtypes = []
         L.fa_oracle_attention.restype = ctypes.c_int
         L.fa_oracle_attention.argtypes = [u16p, u16p, u16p, f64p] + [ctypes.c_int] * 5 + [i64p, ctypes.c_int64, ctypes.c_int]
+        L.fa_oracle_attention_scalar.restype = ctypes.c_int
+        L.fa_oracle_attention_scalar.argtypes = L.fa_oracle_attention.argtypes
         L.fa_oracle_compare.restype = None
         L.fa_oracle_compare.argtypes = [u16p, f64p, ctypes.c_int64, ctypes.c_int, ctypes.POINTER(_Accuracy)]
         L.fa_oracle_quantile_sorted.restype = ctypes.c_double
@@ -211,25 +213,28 @@ def make_inputs(batch, heads, seq_len, head_dim, family: str = "uniform", seeds=
 
 
 # ---------------------------------------------------------------- the oracle
-def attention(q, k, v, causal: bool, rows=None, threads: int = 0) -> np.ndarray:
+def attention(q, k, v, causal: bool, rows=None, threads: int = 0, scalar: bool = False) -> np.ndarray:
     """FP64 attention (bench_flash_attention.cu:105-145).
 
     q, k, v: uint16 bf16 bits [B,H,N,D]. rows: optional global row ids
     (bh*N + query); returns float64 [len(rows), D], else [B,H,N,D].
+    scalar: compute row by row with the direct restatement (slow; the pin of
+    the default blocked path, which must agree with it bit for bit).
     """
     q = np.ascontiguousarray(q)
     k = np.ascontiguousarray(k)
     v = np.ascontiguousarray(v)
     B, H, N, D = q.shape
     assert k.shape == q.shape and v.shape == q.shape
+    fn = lib().fa_oracle_attention_scalar if scalar else lib().fa_oracle_attention
     if rows is None:
         out = np.empty((B, H, N, D), dtype=np.float64)
-        rc = lib().fa_oracle_attention(_u16(q), _u16(k), _u16(v), _f64(out), B, H, N, D, int(causal),
+        rc = fn(_u16(q), _u16(k), _u16(v), _f64(out), B, H, N, D, int(causal),
                                        None, 0, threads)
     else:
         rows = np.ascontiguousarray(rows, dtype=np.int64)
         out = np.empty((rows.size, D), dtype=np.float64)
-        rc = lib().fa_oracle_attention(_u16(q), _u16(k), _u16(v), _f64(out), B, H, N, D, int(causal),
+        rc = fn(_u16(q), _u16(k), _u16(v), _f64(out), B, H, N, D, int(causal),
                                        rows.ctypes.data_as(ctypes.POINTER(ctypes.c_int64)), rows.size, threads)
     if rc != 0:
         raise ValueError("fa_oracle_attention rejected its arguments")

@@ -32,6 +32,7 @@
 // accuracy statistics (results/raw/flash_attention/accuracy.csv:2-21).
 
 #include <algorithm>
+#include <atomic>
 #include <cfloat>
 #include <cmath>
 #include <cstddef>
@@ -144,6 +145,224 @@ void oracle_row(const uint16_t* q, const uint16_t* k, const uint16_t* v, double*
             out_row[dim] += p * static_cast<double>(bf16_to_float(v_row[dim]));
     }
     for (int dim = 0; dim < d; ++dim) out_row[dim] /= sum;
+}
+
+// ---------------------------------------------------------------------------
+// The same arithmetic as oracle_row, reorganised for cache reuse: a group of
+// up to kGroup queries of one slab walks the keys in tiles of kKeyTile, with
+// register blocks of kQB queries x kKB keys (scores) and kQB queries x kDB
+// head dims (P.V). Every score is still the sequential sum over head dims
+// 0..D-1 of double(q)*double(k), times the promoted float scale; every output
+// element is still the sequential sum over keys 0..limit-1 of p*double(v);
+// the max, exp, sum and division run per query in key order. Only the order
+// in which independent sums are advanced changes, so each output is
+// bitwise identical to oracle_row's (tests/test_oracle_pins.py checks that
+// against fa_oracle_attention_scalar). Keys past a query's causal limit are
+// never added into its sums.
+constexpr int kGroup = 64;     // queries per work item
+constexpr int kKeyTile = 256;  // keys per cache tile
+constexpr int kQB = 4;         // queries per register block
+constexpr int kKB = 8;         // keys per score register block
+constexpr int kDB = 8;         // head dims per P.V register block
+
+struct SlabCache
+{
+    int n_pad = 0;           // seq_len rounded up to kKB
+    std::vector<double> kt;  // K^T as double, [head_dim][n_pad], zero padded
+    std::vector<double> vd;  // V as double, [seq_len][head_dim]
+};
+
+void fill_slab_cache(SlabCache& c, const uint16_t* k, const uint16_t* v, int n, int d)
+{
+    c.n_pad = (n + kKB - 1) / kKB * kKB;
+    c.kt.assign(static_cast<size_t>(d) * c.n_pad, 0.0);
+    c.vd.resize(static_cast<size_t>(n) * d);
+    for (int key = 0; key < n; ++key)
+        for (int dim = 0; dim < d; ++dim)
+        {
+            c.kt[static_cast<size_t>(dim) * c.n_pad + key] = bf16_to_float(k[static_cast<size_t>(key) * d + dim]);
+            c.vd[static_cast<size_t>(key) * d + dim] = bf16_to_float(v[static_cast<size_t>(key) * d + dim]);
+        }
+}
+
+// Four doubles in one vector (GCC vector extension): AVX2 registers in the
+// avx2 clone, SSE2 pairs otherwise. Element-wise + and * are plain IEEE
+// double operations (the build uses -ffp-contract=off: no fused forms).
+typedef double v4d __attribute__((vector_size(32)));
+
+__attribute__((always_inline)) inline v4d load4(const double* p)
+{
+    v4d x;
+    std::memcpy(&x, p, sizeof(x));
+    return x;
+}
+
+__attribute__((always_inline)) inline void store4(double* p, v4d x) { std::memcpy(p, &x, sizeof(x)); }
+
+// Scores of kQB queries (qd: [kQB][d] doubles) against keys [key0, key1),
+// key1 - key0 a multiple of kKB, into sc[t * stride + key]. Vector lane j of
+// acc[t][h] is the running dot product of query t with key kb + 4h + j,
+// summed over head dims in increasing order.
+__attribute__((target_clones("avx2", "default"))) void score_block(const double* qd, const double* kt, int n_pad,
+                                                                   int d, int key0, int key1, double scale,
+                                                                   double* sc, int stride)
+{
+    static_assert(kKB == 8, "two vectors of keys per register block");
+    for (int kb = key0; kb < key1; kb += kKB)
+    {
+        v4d acc[kQB][2] = {};
+        for (int dim = 0; dim < d; ++dim)
+        {
+            const double* kr = kt + static_cast<size_t>(dim) * n_pad + kb;
+            const v4d k0 = load4(kr);
+            const v4d k1 = load4(kr + 4);
+            for (int t = 0; t < kQB; ++t)
+            {
+                const v4d qv = v4d{} + qd[t * d + dim];
+                acc[t][0] += qv * k0;
+                acc[t][1] += qv * k1;
+            }
+        }
+        for (int t = 0; t < kQB; ++t)
+        {
+            store4(sc + static_cast<size_t>(t) * stride + kb, acc[t][0] * scale);
+            store4(sc + static_cast<size_t>(t) * stride + kb + 4, acc[t][1] * scale);
+        }
+    }
+}
+
+// out[t][dim] += sum over keys [key0, key1) of p[t][key] * v[key][dim] for
+// kQB queries, keys in increasing order, every dim block of kDB.
+__attribute__((target_clones("avx2", "default"))) void pv_block4(const double* p, int stride, const double* vd,
+                                                                 int d, int key0, int key1, double* out)
+{
+    const int d_full = d / kDB * kDB;
+    for (int d0 = d_full; d0 < d; ++d0)  // head dims past the last full block
+        for (int key = key0; key < key1; ++key)
+            for (int t = 0; t < kQB; ++t)
+                out[t * d + d0] += p[static_cast<size_t>(t) * stride + key] * vd[static_cast<size_t>(key) * d + d0];
+    static_assert(kDB == 8, "two vectors of head dims per register block");
+    for (int d0 = 0; d0 < d_full; d0 += kDB)
+    {
+        v4d acc[kQB][2];
+        for (int t = 0; t < kQB; ++t)
+        {
+            acc[t][0] = load4(out + t * d + d0);
+            acc[t][1] = load4(out + t * d + d0 + 4);
+        }
+        for (int key = key0; key < key1; ++key)
+        {
+            const double* vr = vd + static_cast<size_t>(key) * d + d0;
+            const v4d v0 = load4(vr);
+            const v4d v1 = load4(vr + 4);
+            for (int t = 0; t < kQB; ++t)
+            {
+                const v4d pv = v4d{} + p[static_cast<size_t>(t) * stride + key];
+                acc[t][0] += pv * v0;
+                acc[t][1] += pv * v1;
+            }
+        }
+        for (int t = 0; t < kQB; ++t)
+        {
+            store4(out + t * d + d0, acc[t][0]);
+            store4(out + t * d + d0 + 4, acc[t][1]);
+        }
+    }
+}
+
+// One query's share of keys [key0, key1) (the keys past the smallest causal
+// limit of its register block), same order.
+void pv_row(const double* p, const double* vd, int d, int key0, int key1, double* out)
+{
+    for (int key = key0; key < key1; ++key)
+    {
+        const double pv = p[key];
+        const double* vr = vd + static_cast<size_t>(key) * d;
+        for (int dim = 0; dim < d; ++dim) out[dim] += pv * vr[dim];
+    }
+}
+
+// A group of queries of one slab (q: the slab's Q, queries[i] its query
+// indices, any order); out_rows[i] receives query i's output row.
+void oracle_group(const uint16_t* q, const SlabCache& c, int n, int d, const int* queries, int count, bool causal,
+                  double scale, double* const* out_rows, std::vector<double>& scores, std::vector<double>& qd,
+                  std::vector<double>& acc)
+{
+    const int blocks = (count + kQB - 1) / kQB;
+    const int rows = blocks * kQB;  // padded with copies of the last query
+    const int stride = c.n_pad;
+    scores.resize(static_cast<size_t>(rows) * stride);
+    qd.resize(static_cast<size_t>(rows) * d);
+    acc.assign(static_cast<size_t>(rows) * d, 0.0);
+    std::vector<int> qi(static_cast<size_t>(rows)), lim(static_cast<size_t>(rows));
+    int max_lim = 0;
+    for (int t = 0; t < rows; ++t)
+    {
+        qi[t] = queries[std::min(t, count - 1)];
+        lim[t] = causal ? qi[t] + 1 : n;
+        max_lim = std::max(max_lim, lim[t]);
+        for (int dim = 0; dim < d; ++dim)
+            qd[static_cast<size_t>(t) * d + dim] = bf16_to_float(q[static_cast<size_t>(qi[t]) * d + dim]);
+    }
+
+    // Scores, key tile by key tile (a tile of K^T stays in cache for the group).
+    for (int k0 = 0; k0 < max_lim; k0 += kKeyTile)
+        for (int b = 0; b < blocks; ++b)
+        {
+            int blim = 0;
+            for (int t = b * kQB; t < b * kQB + kQB; ++t) blim = std::max(blim, lim[t]);
+            const int k1 = std::min(k0 + kKeyTile, (blim + kKB - 1) / kKB * kKB);
+            if (k1 > k0)
+                score_block(&qd[static_cast<size_t>(b) * kQB * d], c.kt.data(), c.n_pad, d, k0, k1, scale,
+                            &scores[static_cast<size_t>(b) * kQB * stride], stride);
+        }
+
+    // Row max, exp and sum per query over its own keys, in key order.
+    std::vector<double> sums(static_cast<size_t>(rows));
+    for (int t = 0; t < rows; ++t)
+    {
+        double* sc = &scores[static_cast<size_t>(t) * stride];
+        double row_max = -1.0e300;
+        for (int key = 0; key < lim[t]; ++key) row_max = std::max(row_max, sc[key]);
+        double sum = 0.0;
+        for (int key = 0; key < lim[t]; ++key)
+        {
+            sc[key] = std::exp(sc[key] - row_max);
+            sum += sc[key];
+        }
+        sums[t] = sum;
+    }
+
+    // P.V: the keys every query of a register block sees go through the
+    // blocked kernel, each query's remaining keys through pv_row, tile by
+    // tile, so every sum still runs over keys in increasing order.
+    for (int k0 = 0; k0 < max_lim; k0 += kKeyTile)
+        for (int b = 0; b < blocks; ++b)
+        {
+            int bmin = n, bmax = 0;
+            for (int t = b * kQB; t < b * kQB + kQB; ++t)
+            {
+                bmin = std::min(bmin, lim[t]);
+                bmax = std::max(bmax, lim[t]);
+            }
+            const int k1 = std::min(k0 + kKeyTile, bmax);
+            if (k1 <= k0) continue;
+            const int common = std::min(k1, bmin);
+            if (common > k0)
+                pv_block4(&scores[static_cast<size_t>(b) * kQB * stride], stride, c.vd.data(), d, k0, common,
+                          &acc[static_cast<size_t>(b) * kQB * d]);
+            for (int t = b * kQB; t < b * kQB + kQB; ++t)
+            {
+                const int lo = std::max(k0, common);
+                const int hi = std::min(k1, lim[t]);
+                if (hi > lo)
+                    pv_row(&scores[static_cast<size_t>(t) * stride], c.vd.data(), d, lo, hi,
+                           &acc[static_cast<size_t>(t) * d]);
+            }
+        }
+
+    for (int t = 0; t < count; ++t)
+        for (int dim = 0; dim < d; ++dim) out_rows[t][dim] = acc[static_cast<size_t>(t) * d + dim] / sums[t];
 }
 
 }  // namespace
@@ -305,9 +524,96 @@ uint32_t fa_oracle_mt19937_10000th(void)
 //          otherwise out is [n_rows, head_dim] in the order given.
 // threads: <=0 uses std::thread::hardware_concurrency().
 // Returns 0, or -1 on an invalid argument.
+//
+// The rows are grouped by slab and computed by oracle_group (the blocked
+// form of oracle_row, bitwise identical to it); fa_oracle_attention_scalar
+// below runs oracle_row itself, one row at a time.
 int fa_oracle_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v, double* out,
                         int batch, int heads, int seq_len, int head_dim, int causal,
                         const int64_t* rows, int64_t n_rows, int threads)
+{
+    if (batch < 0 || heads < 0 || seq_len < 0 || head_dim <= 0) return -1;
+    const int64_t total_rows = static_cast<int64_t>(batch) * heads * seq_len;
+    const int64_t work = rows ? n_rows : total_rows;
+    if (work <= 0) return 0;
+    if (rows)
+        for (int64_t i = 0; i < n_rows; ++i)
+            if (rows[i] < 0 || rows[i] >= total_rows) return -1;
+
+    const double scale = static_cast<double>(fa_oracle_default_scale(head_dim));
+    const int64_t slabs = static_cast<int64_t>(batch) * heads;
+
+    // Output positions ordered by (slab, query): slab s owns order[first[s] .. first[s+1]).
+    std::vector<int64_t> order(static_cast<size_t>(work));
+    for (int64_t i = 0; i < work; ++i) order[static_cast<size_t>(i)] = i;
+    auto row_of = [&](int64_t i) { return rows ? rows[i] : i; };
+    if (rows)
+        std::stable_sort(order.begin(), order.end(), [&](int64_t a, int64_t b) { return row_of(a) < row_of(b); });
+    std::vector<int64_t> first(static_cast<size_t>(slabs) + 1, 0);
+    for (int64_t i = 0; i < work; ++i) ++first[static_cast<size_t>(row_of(i) / seq_len) + 1];
+    for (int64_t s = 0; s < slabs; ++s) first[static_cast<size_t>(s) + 1] += first[static_cast<size_t>(s)];
+
+    // Work items: up to kGroup rows of one slab; small per-slab row counts
+    // use smaller groups so every thread gets work.
+    const int nthreads = pick_threads(threads, work);
+    struct Item
+    {
+        int64_t slab, begin, end;
+    };
+    std::vector<Item> items;
+    std::vector<int64_t> used;
+    for (int64_t s = 0; s < slabs; ++s)
+    {
+        const int64_t b = first[static_cast<size_t>(s)], e = first[static_cast<size_t>(s) + 1];
+        if (e == b) continue;
+        used.push_back(s);
+        const int64_t per = std::max<int64_t>(kQB, std::min<int64_t>(kGroup, (e - b) / nthreads + 1));
+        for (int64_t x = b; x < e; x += per) items.push_back(Item{s, x, std::min(e, x + per)});
+    }
+    std::vector<SlabCache> cache(static_cast<size_t>(slabs));
+
+    auto run_pool = [&](size_t count, auto&& fn) {
+        std::atomic<size_t> next{0};
+        auto worker = [&] {
+            for (size_t it = next++; it < count; it = next++) fn(it);
+        };
+        const int t = static_cast<int>(std::min<size_t>(static_cast<size_t>(nthreads), count));
+        std::vector<std::thread> pool;
+        for (int i = 1; i < t; ++i) pool.emplace_back(worker);
+        worker();
+        for (auto& th : pool) th.join();
+    };
+
+    const size_t slab_elems = static_cast<size_t>(seq_len) * head_dim;
+    run_pool(used.size(), [&](size_t u) {
+        const int64_t s = used[u];
+        fill_slab_cache(cache[static_cast<size_t>(s)], k + static_cast<size_t>(s) * slab_elems,
+                        v + static_cast<size_t>(s) * slab_elems, seq_len, head_dim);
+    });
+    run_pool(items.size(), [&](size_t it) {
+        thread_local std::vector<double> scores, qd, acc;
+        const Item& item = items[it];
+        std::vector<int> queries;
+        std::vector<double*> dst;
+        for (int64_t x = item.begin; x < item.end; ++x)
+        {
+            const int64_t i = order[static_cast<size_t>(x)];
+            queries.push_back(static_cast<int>(row_of(i) % seq_len));
+            dst.push_back(out + static_cast<size_t>(i) * head_dim);
+        }
+        oracle_group(q + static_cast<size_t>(item.slab) * slab_elems, cache[static_cast<size_t>(item.slab)],
+                     seq_len, head_dim, queries.data(), static_cast<int>(queries.size()), causal != 0, scale,
+                     dst.data(), scores, qd, acc);
+    });
+    return 0;
+}
+
+// The same contract as fa_oracle_attention, computed row by row with
+// oracle_row (the direct restatement of bench_flash_attention.cu:117-142).
+// Kept as the pin of the blocked path: both must agree bit for bit.
+int fa_oracle_attention_scalar(const uint16_t* q, const uint16_t* k, const uint16_t* v, double* out,
+                               int batch, int heads, int seq_len, int head_dim, int causal,
+                               const int64_t* rows, int64_t n_rows, int threads)
 {
     if (batch < 0 || heads < 0 || seq_len < 0 || head_dim <= 0) return -1;
     const int64_t total_rows = static_cast<int64_t>(batch) * heads * seq_len;

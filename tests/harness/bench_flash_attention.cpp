@@ -36,6 +36,7 @@
 #include <string>
 #include <vector>
 
+#include "fa_mi355x.h"
 #include "flash_attention.h"
 #include "oracle.h"
 
@@ -260,6 +261,20 @@ int main(int argc, char** argv)
             std::printf("  %-14s %8d %6d %8d %8d %11dB %6d %6dB %10d\n", name, d, info.block_size, info.tile_kv,
                         info.rows_per_block, info.shared_bytes_per_block, info.registers_per_thread,
                         info.local_bytes_per_thread, info.max_blocks_per_sm);
+    // Every workgroup configuration of the MFMA kernel (v3 picks one per
+    // shape; the "v3 rows" column of the grid below says which), with the
+    // AGPRs of the compiler's resource report.
+    std::printf("\nMFMA kernel configurations (fa_query_fused):\n  %8s %8s %6s %6s %6s %6s %12s %10s\n", "q_rows",
+                "head_dim", "waves", "block", "VGPRs", "AGPRs", "shared/block", "blocks/CU");
+    for (int rows : {64, 128, 256})
+        for (int d : {64, 128})
+        {
+            fa_tiling_info info{};
+            if (fa_query_fused(d, rows, &info) != 0) return 2;
+            std::printf("  %8d %8d %6d %6d %6d %6d %11dB %10d\n", rows, d, info.waves_per_block, info.block_size,
+                        info.registers_per_thread, info.agprs_per_thread, info.shared_bytes_per_block,
+                        info.max_blocks_per_sm);
+        }
     std::printf("\n");
 
     const std::vector<Entry> table = entries();
@@ -339,9 +354,10 @@ int main(int argc, char** argv)
                     const Problem p{q.bf16(), k.bf16(), v.bf16(), o.bf16(), static_cast<float*>(ws), s, causal};
                     // 4*B*H*N^2*D, halved for causal (BASELINE's convention)
                     const double flops = 4.0 * b * s.heads * static_cast<double>(nlen) * nlen * d * (causal ? 0.5 : 1.0);
-                    std::printf("B=%d H=8 N=%d D=%d %s\n  %-16s %10s %10s %9s %9s %9s\n", b, nlen, d,
-                                causal ? "causal" : "dense", "kernel", "median ms", "IQR ms", "TFLOPS", "HBM GB",
-                                "speedup");
+                    std::printf("B=%d H=8 N=%d D=%d %s (v3 rows per workgroup: %d)\n  %-16s %10s %10s %9s %9s %9s\n",
+                                b, nlen, d, causal ? "causal" : "dense",
+                                fa_tensorcore_v3_rows_per_block(b, 8, nlen, d, causal ? 1 : 0), "kernel", "median ms",
+                                "IQR ms", "TFLOPS", "HBM GB", "speedup");
                     double baseline_ms = 0.0;
                     for (const Entry& e : table)
                     {

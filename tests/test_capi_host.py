@@ -53,11 +53,35 @@ def test_host_models_match_oracle(fa_lib, oracle_mod):
         shape = fa_lib.AttentionShape(B, H, N, D)
         for causal in (False, True):
             assert fa_lib.attention_flops(shape, causal) == oracle_mod.attention_flops(B, H, N, D, causal)
-            assert fa_lib.tensorcore_v3_hbm_bytes(shape, causal) == L.fa_oracle_blocked_kv_hbm_bytes(B, H, N, D, int(causal), 128, 32)
+            # the model follows the configuration the v3 entry runs at this shape
+            rows = fa_lib.tensorcore_v3_rows_per_block(shape, causal)
+            assert rows in (64, 128, 256)
+            assert fa_lib.tensorcore_v3_hbm_bytes(shape, causal) == L.fa_oracle_blocked_kv_hbm_bytes(B, H, N, D, int(causal), rows, 32)
             assert fa_lib.tensorcore_v3b_hbm_bytes(shape, causal) == L.fa_oracle_blocked_kv_hbm_bytes(B, H, N, D, int(causal), 64, 32)
         assert fa_lib.unfused_workspace_bytes(shape) == L.fa_oracle_unfused_workspace_bytes(B, H, N)
     for d in (1, 3, 64, 80, 96, 128, 256):
         assert np.float32(fa_lib.default_scale(d)) == np.float32(oracle_mod.default_scale(d))
+
+
+def test_error_state_records_host_side_rejections(fa_lib):
+    """fa_get_last_error: a host-side rejection is kept for the calling thread
+    until read (hipGetLastError semantics); an unsupported head_dim is silent;
+    an empty shape is a success that leaves the state alone."""
+    L = fa_lib.lib()
+    fake = 0x10000
+    assert fa_lib.get_last_error() in (0, 1)  # earlier tests may have left one
+    assert fa_lib.get_last_error() == 0
+    assert L.fa_launch_attention_tensorcore_v3(fake + 8, fake, fake, fake, 1, 1, 64, 64, 0, None) == 1
+    assert fa_lib.peek_at_last_error() == 1 and fa_lib.peek_at_last_error() == 1
+    assert L.fa_launch_attention_tensorcore_v3(None, None, None, None, 0, 8, 64, 64, 0, None) == 0
+    assert fa_lib.get_last_error() == 1
+    assert fa_lib.get_last_error() == 0
+    assert L.fa_launch_attention_tensorcore_v3(fake, fake, fake, fake, 1, 1, 64, 96, 0, None) == fa_lib.FA_ERROR_UNSUPPORTED
+    assert fa_lib.get_last_error() == 0
+    assert L.fa_launch_attention_unfused(fake, fake, fake, fake, None, 1, 1, 64, 64, 0, None) == 1
+    assert L.fa_launch_softmax_rows_inplace(None, 3, 10, None) == 1
+    assert L.fa_query_fused(64, 96, None) == 1
+    assert fa_lib.get_last_error() == 1 and fa_lib.get_last_error() == 0
 
 
 def test_supported_head_dims(fa_lib):
@@ -89,7 +113,7 @@ def test_argument_validation_before_launch(fa_lib):
     # one (batch, head) slab past 2^31 bytes: DMA offsets within a slab are 32-bit, so it is rejected
     assert L.fa_launch_attention_tensorcore_v3(fake, fake, fake, fake, 1, 1, 1 << 24, 128, 0, None) == 1
     assert L.fa_launch_attention_tensorcore_v3(fake, fake, fake, fake, 1, 1, 1 << 25, 64, 1, None) == 1
-    # the pinned-configuration entry: only 0 (auto), 64 and 128 rows per workgroup
+    # the pinned-configuration entry: only 0 (auto), 64, 128 and 256 rows per workgroup
     for rows in (-1, 1, 32, 96, 512):
         assert L.fa_launch_attention_fused(fake, fake, fake, fake, 1, 1, 64, 64, 0, rows, None) == 1
     assert L.fa_launch_attention_fused(None, None, None, None, 0, 8, 64, 64, 1, 256, None) == 0
@@ -143,3 +167,46 @@ int main() {
     assert out[0] == "34359738368" and out[1] == str(2 * 8 * 2048 * 2048 * 4)
     assert out[2] == "1" and out[3] == "0" and out[5] == "0"
     assert np.float32(float(out[4])) == np.float32(1.0) / np.sqrt(np.float32(128))
+
+
+def test_cpp_caller_sees_host_side_rejections(tmp_path, fa_lib):
+    """A reference-style caller of the void C++ launchers sees a launch this
+    library refuses on the host: a misaligned base and a slab past 2^31
+    bytes (fused), a missing workspace (v0). The rejections happen before any
+    HIP call, so no GPU is needed."""
+    src = tmp_path / "dropin_errors.cpp"
+    src.write_text(r'''
+#include "flash_attention.h"
+#include <cstdio>
+#include <cstdint>
+using namespace cuda_op_lab::flash_attention;
+int main() {
+    auto* base = reinterpret_cast<__hip_bfloat16*>(std::uintptr_t{0x10000});
+    auto* misaligned = reinterpret_cast<__hip_bfloat16*>(std::uintptr_t{0x10008});
+    int fails = 0;
+    if (get_last_error() != hipSuccess) ++fails;                      // clean start
+    launch_attention_tensorcore_v3(misaligned, base, base, base, AttentionShape{1, 1, 64, 64}, false);
+    if (peek_at_last_error() != hipErrorInvalidValue) ++fails;        // visible, not consumed
+    if (get_last_error() != hipErrorInvalidValue) ++fails;
+    if (get_last_error() != hipSuccess) ++fails;                      // consumed
+    launch_attention_tensorcore_v3(base, base, base, base, AttentionShape{1, 1, 1 << 24, 128}, true);
+    if (get_last_error() != hipErrorInvalidValue) ++fails;            // one slab past 2^31 bytes
+    launch_attention_tensorcore_v3b(base, base, base, misaligned, AttentionShape{2, 1, 64, 128}, false);
+    if (get_last_error() != hipErrorInvalidValue) ++fails;
+    launch_attention_unfused(base, base, base, base, nullptr, AttentionShape{1, 1, 64, 64}, false);
+    if (get_last_error() != hipErrorInvalidValue) ++fails;            // v0 without a workspace
+    launch_attention_tensorcore_v3(base, base, base, base, AttentionShape{1, 1, 64, 96}, false);
+    if (get_last_error() != hipSuccess) ++fails;                      // unsupported head_dim: silent
+    std::printf("%d\n", fails);
+    return fails;
+}
+''')
+    exe = tmp_path / "dropin_errors"
+    hipcc = "/opt/rocm/bin/hipcc"
+    if not os.path.exists(hipcc):
+        pytest.skip("hipcc not available")
+    pkg = os.path.dirname(fa_lib.LIB_PATH)
+    subprocess.run([hipcc, "-std=c++17", "-O1", f"-I{REPO}/include", str(src), "-o", str(exe), f"-L{pkg}",
+                    "-lfa_mi355x", f"-Wl,-rpath,{pkg}"], check=True, capture_output=True)
+    res = subprocess.run([str(exe)], capture_output=True, text=True)
+    assert res.returncode == 0 and res.stdout.split() == ["0"], (res.stdout, res.stderr)

@@ -3,15 +3,14 @@ long-sequence stress (config 5), both against the FP64 oracle.
 
 Grid: B in {1,2,4} x N in {512..8192} x D in {64,128} x {dense, causal}, H=8,
 Q/K/V uniform[-1,1) reseeded per shape. The reference checks only finiteness
-at grid scale (benchmarks/bench_flash_attention.cu:673-683); here every case
-goes through the full tolerance gate — all rows for N <= 1024, and for larger
-N a stratified sample (every row of each slab's first and last 64-row query
-tile, which hold the sequence start, the partial tail and the longest causal
-rows, plus 32 seeded random rows per slab).
+at grid scale (benchmarks/bench_flash_attention.cu:673-683); here every output
+row of every case goes through the full tolerance gate against the FP64
+oracle (benchmarks/bench_flash_attention.cu:167-218 compares every element),
+and every element is checked finite after a NaN prefill.
 
 Stress: (1,16,16384,128) causal with Q, K ~ N(0, 3^2) so logits exceed 50 and
-the online-softmax rescale is exercised; V uniform. Sampled rows as above,
-plus the 64 rows of head 0 whose visible logits are largest (|s| > 50).
+the online-softmax rescale is exercised; V uniform. Every row is checked; the
+test also asserts that the inputs do reach |s| > 50.
 """
 import numpy as np
 import pytest
@@ -38,12 +37,6 @@ def grid_seeds(B, N, D):
     return {"q": 11 + base, "k": 22 + base, "v": 33 + base}
 
 
-def rows_for(oracle, B, H, N):
-    if N <= 1024:
-        return None
-    return oracle.sample_rows(B, H, N, rows_per_slab=32, tile=64, seed=N + B)
-
-
 @pytest.mark.parametrize("B", [1, 2, 4])
 @pytest.mark.parametrize("D", [64, 128])
 def test_grid_tolerance(fa, oracle_mod, B, D):
@@ -52,17 +45,16 @@ def test_grid_tolerance(fa, oracle_mod, B, D):
         if b != B or d != D:
             continue
         qb, kb, vb = oracle_mod.make_inputs(B, H, N, D, seeds=grid_seeds(B, N, D))
-        rows = rows_for(oracle_mod, B, H, N)
-        ref = oracle_mod.attention(qb, kb, vb, causal, rows=rows, threads=HOST_THREADS)
+        ref = oracle_mod.attention(qb, kb, vb, causal, threads=HOST_THREADS).reshape(-1, D)
         q, k, v = to_dev(qb), to_dev(kb), to_dev(vb)
         for kernel in KERNELS:
             say("grid", kernel, B, H, N, D, causal)
             out = from_dev(run(fa, kernel, q, k, v, causal)).reshape(-1, D)
-            got = out if rows is None else out[rows]
-            # every element of the full output must be finite (NaN prefill)
+            # every element of the output must be finite (NaN prefill)
             n_bad = int(np.count_nonzero((out & 0x7F80) == 0x7F80))
-            acc = oracle_mod.compare(got, ref)
-            print(f"{kernel} {(B, H, N, D, causal)} ulp={acc.ulp:.2f} gate={acc.abs_gate:.3f} nonfinite={n_bad}")
+            acc = oracle_mod.compare(out, ref)
+            print(f"{kernel} {(B, H, N, D, causal)} rows checked {out.shape[0]}/{B * H * N} ulp={acc.ulp:.2f} "
+                  f"gate={acc.abs_gate:.3f} nonfinite={n_bad}")
             if not acc.passed or n_bad:
                 fails.append((kernel, N, causal, n_bad, acc))
         del q, k, v
@@ -85,20 +77,18 @@ def causal_row_max_logit(qf, kf, scale, chunk=2048):
 def test_long_sequence_stress(fa, oracle_mod):
     B, H, N, D = 1, 16, 16384, 128
     qb, kb, vb = oracle_mod.make_inputs(B, H, N, D, "stress")
-    # Logits reach |s| > 50 (logit std ~9 at sigma 3, D 128): find head 0's
-    # rows with the largest logits and put the 64 largest into the checked
-    # sample, next to the stratified rows of every head.
+    # Logits reach |s| > 50 (logit std ~9 at sigma 3, D 128): an input
+    # property, checked on head 0.
     row_max = causal_row_max_logit(oracle_mod.bf16_to_f32(qb[0, 0]), oracle_mod.bf16_to_f32(kb[0, 0]),
                                    oracle_mod.default_scale(D))
     assert row_max.max() > 50, row_max.max()
-    extreme = np.argsort(row_max)[-64:]
-    rows = np.union1d(oracle_mod.sample_rows(B, H, N, rows_per_slab=32, tile=64, seed=5), extreme).astype(np.int64)
-    ref = oracle_mod.attention(qb, kb, vb, True, rows=rows, threads=HOST_THREADS)
+    ref = oracle_mod.attention(qb, kb, vb, True, threads=HOST_THREADS).reshape(-1, D)
     q, k, v = to_dev(qb), to_dev(kb), to_dev(vb)
     for kernel in KERNELS:
         say("stress", kernel)
         out = from_dev(run(fa, kernel, q, k, v, True)).reshape(-1, D)
         assert int(np.count_nonzero((out & 0x7F80) == 0x7F80)) == 0
-        acc = oracle_mod.compare(out[rows], ref)
-        print(f"stress {kernel} ulp={acc.ulp:.2f} gate={acc.abs_gate:.3f} max_abs={acc.max_abs:.3e}")
+        acc = oracle_mod.compare(out, ref)
+        print(f"stress {kernel} rows checked {out.shape[0]}/{B * H * N} ulp={acc.ulp:.2f} gate={acc.abs_gate:.3f} "
+              f"max_abs={acc.max_abs:.3e}")
         assert acc.passed, (kernel, acc)

@@ -4,8 +4,7 @@
 start beyond 2^32 bytes: every slab offset, K/V descriptor base and output row
 address must be 64-bit. The inputs are drawn uniform[-1,1) on the device (no
 4 GiB host arrays); the first, a middle and the last slab are copied back and
-checked against the FP64 oracle on a stratified row sample (the slab's first
-and last 64-row tiles plus 32 seeded rows), dense and causal, for the v3 entry
+every row of them is checked against the FP64 oracle, dense and causal, for the v3 entry
 (256-row configuration at this grid size for dense, 128-row for causal) and
 the pinned 128-row configuration. The output starts as NaN-pattern fill, so a
 slab the kernel skips fails the check."""
@@ -28,16 +27,15 @@ def test_tensors_past_4_gib(fa, oracle_mod):
     say("large inputs", B, H, N, D)
     q, k, v = (torch.empty((B, H, N, D), dtype=torch.bfloat16, device="cuda").uniform_(-1.0, 1.0, generator=gen)
                for _ in range(3))
-    rows = oracle_mod.sample_rows(1, 1, N, rows_per_slab=32, tile=64, seed=99)
     slabs = (0, H // 2 + 1, H - 1)
     host = {s: tuple(from_dev(t[0, s]).reshape(1, 1, N, D) for t in (q, k, v)) for s in slabs}
     for causal in (False, True):
-        refs = {s: oracle_mod.attention(*host[s], causal, rows=rows) for s in slabs}
+        refs = {s: oracle_mod.attention(*host[s], causal).reshape(N, D) for s in slabs}
         for kernel in ("v3_mfma", "v3_128"):
             say("large", kernel, causal)
             o = run(fa, kernel, q, k, v, causal, out=nan_like(q))
             for s in slabs:
-                got = from_dev(o[0, s]).reshape(N, D)[rows]
+                got = from_dev(o[0, s]).reshape(N, D)
                 check(oracle_mod, got, refs[s], f"large {kernel} causal={causal} slab {s}")
             del o
             torch.cuda.empty_cache()

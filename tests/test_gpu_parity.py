@@ -203,9 +203,11 @@ def test_v3_picks_the_configuration_by_grid(fa, oracle_mod):
         ((1, 2 * cus // 32, 8192, 128), (True,), "v3_256"),     # causal, 2 * `cus` of 256 rows
         ((1, 4 * cus // 16, 4096, 128), (True,), "v3_128"),     # causal below 8192 keys
     ]
+    rows_of = {"v3b_mfma": 64, "v3_128": 128, "v3_256": 256}
     for (B, H, N, D), masks, pinned in cases:
         q, k, v = (to_dev(x) for x in oracle_mod.make_inputs(B, H, N, D))
         for causal in masks:
+            assert fa.tensorcore_v3_rows_per_block(fa.AttentionShape(B, H, N, D), causal) == rows_of[pinned]
             say("v3 dispatch", B, H, N, D, causal, pinned)
             a = from_dev(run(fa, "v3_mfma", q, k, v, causal))
             b = from_dev(run(fa, pinned, q, k, v, causal))
@@ -303,9 +305,14 @@ def test_error_paths_leave_output_untouched(fa, oracle_mod):
     assert np.all(from_dev(o) == 0xFFFF)
     # empty sequence: success, no launch
     assert fa.launch_attention_tensorcore_v3(q, q, q, o, fa.AttentionShape(1, 1, 0, 64), False)
-    # misaligned base pointer is rejected on the host
+    # misaligned base pointer is rejected on the host, and kept for the
+    # thread's get_last_error (what a caller of the void C++ launcher reads)
+    fa.get_last_error()
     with pytest.raises(fa.FaError):
         fa.launch_attention_tensorcore_v3(q.data_ptr() + 2, q, q, o, fa.AttentionShape(1, 1, 16, 64), False)
+    assert fa.get_last_error() == 1 and fa.get_last_error() == 0
+    torch.cuda.synchronize()
+    assert np.all(from_dev(o) == 0xFFFF)
     # v0 handles any head_dim, including 96
     qb, kb, vb = oracle_mod.make_inputs(1, 2, 50, 96)
     ref = oracle_mod.attention(qb, kb, vb, True)
@@ -329,3 +336,6 @@ def test_query_reports_resources(fa):
             assert info["max_blocks_per_sm"] >= 1
             assert info["device_shared_bytes_per_sm"] >= 64 * 1024
             assert info["compute_units"] > 0
+            # AGPRs from the compiler's report of the kernel (the kernels
+            # accumulate MFMA results in architectural VGPRs: 0)
+            assert info["agprs_per_thread"] == 0

@@ -105,6 +105,94 @@ def test_flops_and_workspace_identities(oracle_mod):
     assert L.fa_oracle_blocked_kv_hbm_bytes(1, 1, 64, 64, 0, 64, 64) == 4 * 64 * 64 * 2
 
 
+def _reference_hbm_rows():
+    with open(os.path.join(HERE, "golden", "reference_hbm_model.json")) as fh:
+        return json.load(fh)["rows"]
+
+
+def _oracle_model_bytes(L, kernel, B, H, N, D, causal, rows=None, tile=None):
+    """The oracle's byte model for one kernel of the reference's summary.csv
+    (benchmarks/bench_flash_attention.cu:641-648), with the reference's
+    tiling unless `rows` / `tile` override it."""
+    if kernel == "v0_unfused":
+        return L.fa_oracle_qkvo_bytes(B, H, N, D) + L.fa_oracle_unfused_score_bytes(B, H, N)
+    if kernel in ("v2a_fused_tiled", "v2b_fused_tiled"):  # 256 threads / 32 = 8 rows, tileKV 64
+        rows, tile = rows or 8, tile or 64
+    else:  # v3: q_rows 64, v3_tile_kv(D) = 64 (D <= 64) or 32
+        rows, tile = rows or 64, tile or (64 if D <= 64 else 32)
+    return L.fa_oracle_blocked_kv_hbm_bytes(B, H, N, D, causal, rows, tile)
+
+
+def test_byte_models_reproduce_reference_published_hbm(oracle_mod):
+    """All 240 published algorithmic_hbm_gb values (v0, v2a, v2b, v3 rows of
+    results/raw/flash_attention/summary.csv, 60 shapes each) come out of the
+    oracle's byte models to 1e-12."""
+    L = oracle_mod.lib()
+    rows = _reference_hbm_rows()
+    assert len(rows) == 240
+    for r in rows:
+        got = _oracle_model_bytes(L, r["kernel"], r["batch"], r["heads"], r["seq_len"], r["head_dim"], r["causal"])
+        want = float(r["algorithmic_hbm_gb"]) * 1e9
+        assert got == pytest.approx(want, rel=1e-12), r
+
+
+def test_byte_model_fixture_rejects_planted_mistakes(oracle_mod):
+    """The fixture discriminates the model's parameters: the wrong rows per
+    block, or v0 without the softmax passes, each miss published values.
+    (The tile size cancels on the published grid, whose rows per block are
+    multiples of the tile; test_byte_model_closed_forms pins it.)"""
+    L = oracle_mod.lib()
+    rows = _reference_hbm_rows()
+
+    def misses(fn):
+        return sum(1 for r in rows if fn(r) != pytest.approx(float(r["algorithmic_hbm_gb"]) * 1e9, rel=1e-12))
+
+    assert misses(lambda r: _oracle_model_bytes(L, r["kernel"], r["batch"], r["heads"], r["seq_len"], r["head_dim"],
+                                                r["causal"], rows=128) if r["kernel"] != "v0_unfused" else
+                  float(r["algorithmic_hbm_gb"]) * 1e9) > 100
+    assert misses(lambda r: L.fa_oracle_qkvo_bytes(r["batch"], r["heads"], r["seq_len"], r["head_dim"]) +
+                  3.0 / 5.0 * L.fa_oracle_unfused_score_bytes(r["batch"], r["heads"], r["seq_len"])
+                  if r["kernel"] == "v0_unfused" else float(r["algorithmic_hbm_gb"]) * 1e9) == 60
+
+
+def test_byte_model_closed_forms(oracle_mod):
+    """Branches the published grid (N a multiple of every tile) leaves open:
+    ragged N and the causal clamp of the last block's key limit to N-1."""
+    L = oracle_mod.lib()
+    assert L.fa_oracle_unfused_score_bytes(2, 8, 2048) == 20.0 * 2 * 8 * 2048 ** 2
+    for (B, H, N, D, rows, tile) in [(1, 1, 1, 64, 64, 32), (2, 3, 77, 128, 128, 32), (1, 2, 1000, 64, 64, 64),
+                                     (3, 1, 4097, 128, 256, 32), (1, 1, 33, 64, 8, 64)]:
+        nb = -(-N // rows)
+        qo = 2.0 * B * H * N * D * 2
+        # dense: every block loads ceil(N / tile) whole tiles
+        dense = qo + 2.0 * B * H * nb * (-(-N // tile)) * tile * D * 2
+        assert L.fa_oracle_blocked_kv_hbm_bytes(B, H, N, D, 0, rows, tile) == dense
+        # causal: block b loads tiles up to min(last row of b, N-1)
+        tiles = sum(min(b * rows + rows - 1, N - 1) // tile + 1 for b in range(nb))
+        assert L.fa_oracle_blocked_kv_hbm_bytes(B, H, N, D, 1, rows, tile) == qo + 2.0 * B * H * tiles * tile * D * 2
+    # causal, rows == tile, N a multiple: triangular number of tiles
+    assert L.fa_oracle_blocked_kv_hbm_bytes(1, 1, 64 * 10, 64, 1, 64, 64) == (2 * 640 * 64 * 2 +
+                                                                               2 * 55 * 64 * 64 * 2)
+
+
+def test_package_quantiles_and_summary_match_numpy(fa_lib):
+    """The package's type-7 quantile and median/IQR summary (every median in
+    bench.py's line) against numpy's default (linear = type 7) percentile."""
+    rng = np.random.default_rng(11)
+    for n in (1, 2, 3, 7, 30, 31):
+        xs = list(rng.random(n) * 10)
+        for p in (0.0, 0.1, 0.25, 0.5, 0.75, 0.9, 1.0):
+            assert fa_lib.quantile_type7(xs, p) == pytest.approx(float(np.percentile(xs, 100 * p)), rel=1e-14)
+        s = fa_lib.summarize(xs)
+        q1, med, q3 = np.percentile(xs, [25, 50, 75])
+        assert s["median_ms"] == pytest.approx(med, rel=1e-14)
+        assert s["q1_ms"] == pytest.approx(q1, rel=1e-14) and s["q3_ms"] == pytest.approx(q3, rel=1e-14)
+        assert s["iqr_ms"] == pytest.approx(q3 - q1, rel=1e-12, abs=1e-15)
+    # order of the samples does not matter; ties and a known small case
+    assert fa_lib.quantile_type7([4.0, 1.0, 3.0, 2.0], 0.25) == 1.75
+    assert fa_lib.summarize([2.0, 2.0, 2.0])["iqr_ms"] == 0.0
+
+
 def test_quantile_type7(oracle_mod):
     rng = np.random.default_rng(5)
     for n in (1, 2, 7, 30):
@@ -189,6 +277,28 @@ def test_row_subset_matches_full(oracle_mod):
     assert np.array_equal(part, full[rows])
     with pytest.raises(ValueError):
         oracle_mod.attention(q, k, v, True, rows=np.array([280], dtype=np.int64))
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_blocked_path_equals_scalar_restatement(oracle_mod, causal):
+    """The default (cache-blocked) oracle reorders only which independent sums
+    advance first; every output must equal the row-by-row restatement of
+    bench_flash_attention.cu:117-142 bit for bit: ragged N (tails of the
+    4-query, 8-key and 256-key blocks), head dims that are not a multiple of
+    8, several slabs, unsorted and repeated row lists, several families."""
+    cases = [((1, 1, 1, 64), "uniform"), ((2, 3, 37, 128), "uniform"), ((1, 2, 300, 64), "stress"),
+             ((1, 1, 513, 128), "normal_mt19937"), ((2, 1, 77, 5), "uniform"), ((1, 2, 260, 80), "scaled"),
+             ((1, 1, 129, 3), "ramp")]
+    for shape, family in cases:
+        q, k, v = oracle_mod.make_inputs(*shape, family)
+        fast = oracle_mod.attention(q, k, v, causal, threads=4)
+        slow = oracle_mod.attention(q, k, v, causal, threads=4, scalar=True)
+        assert np.array_equal(fast.view(np.uint64), slow.view(np.uint64)), (shape, family, causal)
+        total = shape[0] * shape[1] * shape[2]
+        rows = np.random.default_rng(total).integers(0, total, size=min(total, 50)).astype(np.int64)
+        rows = np.concatenate([rows, rows[:3]])  # repeats and any order
+        part = oracle_mod.attention(q, k, v, causal, rows=rows, threads=3)
+        assert np.array_equal(part.view(np.uint64), slow.reshape(-1, shape[3])[rows].view(np.uint64))
 
 
 def _reference_cases():
