@@ -15,8 +15,20 @@
 //     BASELINE's gate (abs_gate <= 1: |O - O_ref| <= 2^-7 max|O_ref row|).
 // Test infrastructure: the FP64 oracle (oracle/liboracle.so) is the checker.
 //
-// Usage: bench_flash_attention [--quick] [output_directory]
-//   --quick  B = 1, N in {512, 2048} only (eight grid cases).
+// Usage: bench_flash_attention [--quick | --accuracy-only] [output_directory]
+//        bench_flash_attention --v0-profile [--check] [output_directory]
+//   --quick          B = 1, N in {512, 2048} only (eight grid cases).
+//   --accuracy-only  the accuracy suite alone (the ctest).
+//   --v0-profile     the v0 stage profile (benchmarks/profile_attention_v0.cu):
+//                    the instrumented launch must equal the plain one bit for
+//                    bit (with events, on a non-default stream, and without
+//                    events); then, at the reference's two profiling shapes,
+//                    30 samples (5 warmups) of the per-stage times (QK,
+//                    softmax, PV), the instrumented pipeline and an
+//                    unmarked v0 launch, written as v0_stage_timing.csv with
+//                    the reference's columns. With --check: the bitwise
+//                    checks alone, at N in {1, 17, 256}, D in {64, 128},
+//                    dense and causal.
 // Exit status: 0 when every accuracy row passes both gates and every timed
 // output is finite, 1 otherwise, 2 on a usage or HIP error.
 
@@ -38,6 +50,7 @@
 
 #include "fa_mi355x.h"
 #include "flash_attention.h"
+#include "flash_attention_v0_profile.h"
 #include "oracle.h"
 
 namespace fa = cuda_op_lab::flash_attention;
@@ -214,20 +227,126 @@ uint64_t grid_seed(uint64_t tensor_seed, const fa::AttentionShape& s)
     return tensor_seed + 1000ull * s.batch + 10ull * (s.seq_len / 512) + s.head_dim;
 }
 
+double quantile_of(std::vector<double> xs, double p)
+{
+    std::sort(xs.begin(), xs.end());
+    return fa_oracle_quantile_sorted(xs.data(), static_cast<int64_t>(xs.size()), p);
+}
+
+// One v0 stage-profile shape: bitwise check of the instrumented launch
+// against the plain one, then (unless check_only) the stage timings.
+// Returns false on a mismatch.
+bool v0_profile_shape(const fa::AttentionShape& s, bool causal, bool check_only, std::ostream* csv)
+{
+    const size_t n = elements(s);
+    std::vector<uint16_t> host(n), plain(n), got(n);
+    DeviceBuffer q(n * 2), k(n * 2), v(n * 2), o(n * 2), ws(std::max<size_t>(4, fa::unfused_workspace_bytes(s)));
+    fa_oracle_fill_normal_mt19937(host.data(), static_cast<int64_t>(n), 11u);
+    HIP_OK(hipMemcpy(q.ptr, host.data(), n * 2, hipMemcpyHostToDevice));
+    fa_oracle_fill_normal_mt19937(host.data(), static_cast<int64_t>(n), 22u);
+    HIP_OK(hipMemcpy(k.ptr, host.data(), n * 2, hipMemcpyHostToDevice));
+    fa_oracle_fill_normal_mt19937(host.data(), static_cast<int64_t>(n), 33u);
+    HIP_OK(hipMemcpy(v.ptr, host.data(), n * 2, hipMemcpyHostToDevice));
+    float* wsp = static_cast<float*>(ws.ptr);
+    hipStream_t stream = nullptr;
+    HIP_OK(hipStreamCreate(&stream));
+    hipEvent_t ev[6];
+    for (auto& e : ev) HIP_OK(hipEventCreate(&e));
+    const fa::V0ProfileEvents events{ev[0], ev[1], ev[2], ev[3]};
+
+    HIP_OK(hipMemset(o.ptr, 0xff, n * 2));
+    fa::launch_attention_unfused(q.bf16(), k.bf16(), v.bf16(), o.bf16(), wsp, s, causal, stream);
+    HIP_OK(hipGetLastError());
+    HIP_OK(hipStreamSynchronize(stream));
+    HIP_OK(hipMemcpy(plain.data(), o.ptr, n * 2, hipMemcpyDeviceToHost));
+    bool same = true;
+    for (const fa::V0ProfileEvents* e : {&events, static_cast<const fa::V0ProfileEvents*>(nullptr)})
+    {
+        HIP_OK(hipMemset(o.ptr, 0xff, n * 2));
+        HIP_OK(fa::launch_attention_unfused_profile(q.bf16(), k.bf16(), v.bf16(), o.bf16(), wsp, s, causal, e,
+                                                    stream));
+        HIP_OK(hipStreamSynchronize(stream));
+        HIP_OK(hipMemcpy(got.data(), o.ptr, n * 2, hipMemcpyDeviceToHost));
+        size_t nan = 0, inf = 0;
+        count_nonfinite(got, nan, inf);
+        same = same && nan == 0 && inf == 0 && std::memcmp(got.data(), plain.data(), n * 2) == 0;
+    }
+    std::printf("v0 profile B=%d H=%d N=%d D=%d causal=%d: %s\n", s.batch, s.heads, s.seq_len, s.head_dim,
+                causal ? 1 : 0, same ? "PASS (finite, bitwise equal to v0)" : "FAIL");
+    if (same && !check_only)
+    {
+        constexpr int kSamples = 30;
+        for (int i = 0; i < kWarmup; ++i)
+        {
+            fa::launch_attention_unfused(q.bf16(), k.bf16(), v.bf16(), o.bf16(), wsp, s, causal, stream);
+            HIP_OK(fa::launch_attention_unfused_profile(q.bf16(), k.bf16(), v.bf16(), o.bf16(), wsp, s, causal,
+                                                        nullptr, stream));
+        }
+        HIP_OK(hipGetLastError());
+        HIP_OK(hipStreamSynchronize(stream));
+        std::vector<double> t[5];
+        for (int i = 0; i < kSamples; ++i)
+        {
+            // an unmarked v0 launch between its own events, then the instrumented one
+            HIP_OK(hipEventRecord(ev[4], stream));
+            fa::launch_attention_unfused(q.bf16(), k.bf16(), v.bf16(), o.bf16(), wsp, s, causal, stream);
+            HIP_OK(hipEventRecord(ev[5], stream));
+            HIP_OK(fa::launch_attention_unfused_profile(q.bf16(), k.bf16(), v.bf16(), o.bf16(), wsp, s, causal,
+                                                        &events, stream));
+            HIP_OK(hipEventSynchronize(ev[3]));
+            const std::pair<int, int> spans[5] = {{0, 1}, {1, 2}, {2, 3}, {0, 3}, {4, 5}};
+            for (int m = 0; m < 5; ++m)
+            {
+                float ms = 0.0f;
+                HIP_OK(hipEventElapsedTime(&ms, ev[spans[m].first], ev[spans[m].second]));
+                t[m].push_back(ms);
+            }
+        }
+        const char* labels[5] = {"QK", "softmax", "PV", "instrumented_pipeline", "original_v0_e2e"};
+        const double pipeline = quantile_of(t[3], 0.5);
+        char tag[64];
+        std::snprintf(tag, sizeof(tag), "b%dh%dn%dd%d_%s", s.batch, s.heads, s.seq_len, s.head_dim,
+                      causal ? "causal" : "dense");
+        std::printf("  %-22s %10s %10s %10s %10s %7s\n", "metric", "median_ms", "q1_ms", "q3_ms", "iqr_ms", "share");
+        for (int m = 0; m < 5; ++m)
+        {
+            const double med = quantile_of(t[m], 0.5), q1 = quantile_of(t[m], 0.25), q3 = quantile_of(t[m], 0.75);
+            std::printf("  %-22s %10.6f %10.6f %10.6f %10.6f", labels[m], med, q1, q3, q3 - q1);
+            *csv << tag << ',' << s.batch << ',' << s.heads << ',' << s.seq_len << ',' << s.head_dim << ','
+                 << (causal ? 1 : 0) << ',' << labels[m] << ',' << med << ',' << q1 << ',' << q3 << ',' << q3 - q1
+                 << ',';
+            if (m < 4)
+            {
+                std::printf(" %7.4f", med / pipeline);
+                *csv << med / pipeline;
+            }
+            std::printf("\n");
+            *csv << '\n';
+        }
+    }
+    for (auto& e : ev) HIP_OK(hipEventDestroy(e));
+    HIP_OK(hipStreamDestroy(stream));
+    return same;
+}
+
 }  // namespace
 
 int main(int argc, char** argv)
 {
-    bool quick = false;
+    bool quick = false, accuracy_only = false, v0_profile = false, check_only = false;
     std::filesystem::path out_dir = "results/raw/flash_attention";
     for (int a = 1; a < argc; ++a)
     {
         const std::string arg = argv[a];
         if (arg == "--quick") quick = true;
-        else if (arg == "--help" || arg == "-h")
+        else if (arg == "--accuracy-only") accuracy_only = true;
+        else if (arg == "--v0-profile") v0_profile = true;
+        else if (arg == "--check") check_only = true;
+        else if (arg == "--help" || arg == "-h" || arg.rfind("--", 0) == 0)
         {
-            std::printf("usage: %s [--quick] [output_directory]\n", argv[0]);
-            return 0;
+            std::printf("usage: %s [--quick | --accuracy-only] [output_directory]\n"
+                        "       %s --v0-profile [--check] [output_directory]\n", argv[0], argv[0]);
+            return arg.rfind("--h", 0) == 0 || arg == "-h" ? 0 : 2;
         }
         else out_dir = arg;
     }
@@ -237,6 +356,28 @@ int main(int argc, char** argv)
     {
         std::fprintf(stderr, "cannot create %s: %s\n", out_dir.string().c_str(), ec.message().c_str());
         return 2;
+    }
+    if (v0_profile)
+    {
+        bool ok = true;
+        std::ofstream stage_csv;
+        if (!check_only)
+            stage_csv = open_csv(out_dir / "v0_stage_timing.csv",
+                                 "shape,batch,heads,seq_len,head_dim,causal,metric,median_ms,q1_ms,q3_ms,iqr_ms,"
+                                 "share_of_pipeline");
+        if (check_only)
+        {
+            for (int n : {1, 17, 256})
+                for (int d : {64, 128})
+                    for (bool causal : {false, true}) ok = v0_profile_shape({1, 2, n, d}, causal, true, nullptr) && ok;
+        }
+        else
+        {
+            // the reference's two profiling shapes (results/raw/v0_stage_timing.csv)
+            ok = v0_profile_shape({2, 8, 2048, 64}, false, false, &stage_csv) && ok;
+            ok = v0_profile_shape({1, 8, 2048, 128}, false, false, &stage_csv) && ok;
+        }
+        return ok ? 0 : 1;
     }
     auto raw_csv = open_csv(out_dir / "raw_timings.csv", "kernel,batch,heads,seq_len,head_dim,causal,iteration,elapsed_ms");
     auto summary_csv = open_csv(out_dir / "summary.csv",
@@ -323,6 +464,11 @@ int main(int argc, char** argv)
         }
     accuracy_csv.flush();
     std::printf("\n");
+    if (accuracy_only)
+    {
+        std::printf("%s\n", all_ok ? "accuracy suite passed" : "accuracy suite FAILED");
+        return all_ok ? 0 : 1;
+    }
 
     // Timed grid.
     std::vector<int> batches = {1, 2, 4}, lengths = {512, 1024, 2048, 4096, 8192};
