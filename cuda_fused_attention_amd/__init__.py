@@ -82,6 +82,8 @@ _SIGNATURES = {
     "fa_attention_flops": (ctypes.c_double, [_i, _i, _i, _i, _i]),
     "fa_unfused_workspace_bytes": (ctypes.c_size_t, [_i, _i, _i, _i]),
     "fa_launch_attention_unfused": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp]),
+    "fa_launch_attention_unfused_noalloc": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp]),
+    "fa_unfused_noalloc_max_workspace_bytes": (ctypes.c_size_t, []),
     "fa_launch_softmax_rows_inplace": (_i, [_vp, _i, _i, _vp]),
     "fa_launch_attention_unfused_profile": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp, _vp]),
     "fa_tensorcore_v3_supported": (_i, [_i]),

@@ -14,6 +14,7 @@
 //     (write S, read S, write P, read P) against the reference's 5 passes.
 // Algorithmic bytes per launch: 16*B*H*N^2 + 8*B*H*N*D (HBM roofline).
 
+#include <atomic>
 #include <cfloat>
 #include <cstdint>
 
@@ -364,13 +365,16 @@ int launch_softmax(float* s, int rows, int cols, hipStream_t stream)
     return fa::launch_kernel(v0_softmax_rows_loop_kernel, grid, block, stream, s, cols);
 }
 
-int validate_unfused(const void* q, const void* k, const void* v, void* o, const float* workspace,
-                     int batch, int heads, int seq_len, int head_dim)
+// Shape and pointer checks shared by the v0 entry points (the workspace is
+// checked by the caller): hipSuccess, -1 for an empty shape (nothing to
+// launch) or hipErrorInvalidValue.
+int validate_unfused(const void* q, const void* k, const void* v, void* o, int batch, int heads, int seq_len,
+                     int head_dim)
 {
     if (batch < 0 || heads < 0 || seq_len < 0 || head_dim <= 0) return hipErrorInvalidValue;
     const long long bh = static_cast<long long>(batch) * heads;
     if (bh == 0 || seq_len == 0) return -1;  // empty: nothing to launch
-    if (!q || !k || !v || !o || !workspace) return hipErrorInvalidValue;
+    if (!q || !k || !v || !o) return hipErrorInvalidValue;
     if (bh > kMaxGridY) return hipErrorInvalidValue;
     const long long tiles = (static_cast<long long>(seq_len) + kTile - 1) / kTile;
     if (tiles * tiles > 0x7fffffffLL) return hipErrorInvalidValue;
@@ -382,9 +386,10 @@ int launch_unfused_impl(const void* q, const void* k, const void* v, void* o, fl
                         int heads, int seq_len, int head_dim, int causal, hipEvent_t const* events,
                         hipStream_t stream)
 {
-    const int status = validate_unfused(q, k, v, o, workspace, batch, heads, seq_len, head_dim);
+    const int status = validate_unfused(q, k, v, o, batch, heads, seq_len, head_dim);
     if (status == -1) return hipSuccess;
     if (status != hipSuccess) return status;
+    if (!workspace) return hipErrorInvalidValue;
 
     const int bh = batch * heads;
     const int n = seq_len;
@@ -423,9 +428,73 @@ int launch_unfused_impl(const void* q, const void* k, const void* v, void* o, fl
     return hipSuccess;
 }
 
+// The allocation-free v0 entry point's score workspace: a file-scope device
+// array, one copy per GPU, held for the life of the process. In host code
+// its name is only a stand-in for the symbol; the device address is looked
+// up once per device (noalloc_scratch) and only that address is used.
+constexpr size_t kNoAllocScratchBytes = size_t{64} << 20;
+__device__ __align__(256) float scratch[kNoAllocScratchBytes / sizeof(float)];
+
+constexpr int kMaxDevices = 64;
+
+// Device address of `scratch` on the current device (hipGetSymbolAddress,
+// once per device, cached), or null with the HIP status in *status.
+float* noalloc_scratch(int* status)
+{
+    static std::atomic<uintptr_t> cache[kMaxDevices];
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    {
+        *status = e != hipSuccess ? e : hipErrorInvalidDevice;
+        return nullptr;
+    }
+    uintptr_t addr = cache[dev].load(std::memory_order_acquire);
+    if (addr == 0)
+    {
+        void* ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || ptr == nullptr)
+        {
+            *status = e != hipSuccess ? e : hipErrorInvalidSymbol;
+            return nullptr;
+        }
+        addr = reinterpret_cast<uintptr_t>(ptr);
+        cache[dev].store(addr, std::memory_order_release);
+    }
+    *status = hipSuccess;
+    return reinterpret_cast<float*>(addr);
+}
+
+int launch_unfused_noalloc(const void* q, const void* k, const void* v, void* o, int batch, int heads, int seq_len,
+                           int head_dim, int causal, hipStream_t stream)
+{
+    // The same checks as the workspace entry, minus the workspace pointer.
+    int status = validate_unfused(q, k, v, o, batch, heads, seq_len, head_dim);
+    if (status == -1) return hipSuccess;
+    if (status != hipSuccess) return status;
+    const size_t need = fa_unfused_workspace_bytes(batch, heads, seq_len, head_dim);
+    if (need > kNoAllocScratchBytes) return hipErrorInvalidValue;
+    float* ws = noalloc_scratch(&status);
+    if (!ws) return status;
+    // The scores kernel writes every element of S the softmax and PV kernels
+    // read (masked ones as -FLT_MAX), so the array needs no clearing between
+    // calls.
+    return launch_unfused_impl(q, k, v, o, ws, batch, heads, seq_len, head_dim, causal, nullptr, stream);
+}
+
 }  // namespace
 
 extern "C" {
+
+size_t fa_unfused_noalloc_max_workspace_bytes(void) { return kNoAllocScratchBytes; }
+
+int fa_launch_attention_unfused_noalloc(const void* q, const void* k, const void* v, void* o, int batch, int heads,
+                                        int seq_len, int head_dim, int causal, void* stream)
+{
+    return fa::record_status(launch_unfused_noalloc(q, k, v, o, batch, heads, seq_len, head_dim, causal,
+                                                    static_cast<hipStream_t>(stream)));
+}
 
 float fa_default_scale(int head_dim) { return 1.0f / sqrtf(static_cast<float>(head_dim)); }
 

@@ -93,6 +93,22 @@ int fa_launch_attention_unfused(const void* q, const void* k, const void* v, voi
                                 float* workspace, int batch, int heads, int seq_len,
                                 int head_dim, int causal, void* stream);
 
+/* No counterpart in the reference. For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): fa_launch_attention_unfused without the workspace
+ * argument. The score workspace is a 64 MiB array inside the library, one
+ * per GPU, held until the process ends; shapes needing more
+ * (fa_unfused_workspace_bytes > fa_unfused_noalloc_max_workspace_bytes(),
+ * e.g. B*H*N*N > 16M) return hipErrorInvalidValue and launch nothing. It
+ * calls no allocator. Every call on one GPU uses that GPU's one array:
+ * calls that overlap on one GPU (two streams, two threads) race and must be
+ * serialised by the caller. Same kernels, so the same output bits as the
+ * workspace entry. */
+int fa_launch_attention_unfused_noalloc(const void* q, const void* k, const void* v, void* o,
+                                        int batch, int heads, int seq_len, int head_dim,
+                                        int causal, void* stream);
+size_t fa_unfused_noalloc_max_workspace_bytes(void);
+
 /* include/flash_attention.h:36, kernels/v0_unfused.cu:133-138 — stable row
  * softmax in place over a [rows, cols] fp32 matrix. */
 int fa_launch_softmax_rows_inplace(float* s, int rows, int cols, void* stream);
