@@ -324,7 +324,7 @@ def main():
             v0["algorithmic_bytes"] = v0_bytes
             v0["reference_model_bytes"] = 20.0 * b * h * n * n + 8.0 * b * h * n * d
             entry["v0_unfused"] = v0
-            entry["v3_rows_per_block"] = fa.tensorcore_v3_rows_per_block(sh, c)
+            entry["v3_config"] = dict(zip(("rows_per_block", "kv_groups"), fa.tensorcore_v3_config(sh, c)))
             # Back-to-back: the kernel's own duration, without the ~7 us of
             # idle-queue dispatch each individually timed launch carries.
             flops_s = baseline_flops(b, h, n, d, c)

@@ -33,8 +33,11 @@ KERNEL_V3 = 1
 KERNEL_V3B = 2
 KERNEL_V3_128 = 3  # the fused forward pinned to 128 rows per workgroup
 KERNEL_V3_256 = 4  # pinned to 256 rows per workgroup (one wave group)
+KERNEL_V3_64X4 = 5  # pinned to 64 rows per workgroup split over four KV groups (head_dim 64)
 KERNEL_IDS = {"v0_unfused": KERNEL_UNFUSED, "v3_mfma": KERNEL_V3, "v3b_mfma": KERNEL_V3B, "v3_128": KERNEL_V3_128,
-              "v3_256": KERNEL_V3_256}
+              "v3_256": KERNEL_V3_256, "v3_64x4": KERNEL_V3_64X4}
+# (rows per workgroup, KV groups) of each pinned fused configuration
+FUSED_CONFIGS = {"v3b_mfma": (64, 2), "v3_128": (128, 2), "v3_256": (256, 1), "v3_64x4": (64, 4)}
 
 _lib = None
 
@@ -64,7 +67,7 @@ class TilingInfo(ctypes.Structure):
             "supported", "block_size", "tile_kv", "rows_per_block", "shared_bytes_per_block",
             "registers_per_thread", "local_bytes_per_thread", "max_blocks_per_sm",
             "device_shared_bytes_per_sm", "shared_limited_blocks_per_sm", "agprs_per_thread",
-            "waves_per_block", "compute_units",
+            "waves_per_block", "compute_units", "kv_groups",
         )
     ]
 
@@ -90,7 +93,10 @@ _SIGNATURES = {
     "fa_launch_attention_tensorcore_v3": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp]),
     "fa_launch_attention_fused": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp]),
     "fa_query_fused": (_i, [_i, _i, ctypes.POINTER(TilingInfo)]),
+    "fa_launch_attention_fused_groups": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp]),
+    "fa_query_fused_groups": (_i, [_i, _i, _i, ctypes.POINTER(TilingInfo)]),
     "fa_tensorcore_v3_rows_per_block": (_i, [_i, _i, _i, _i, _i]),
+    "fa_tensorcore_v3_config": (_i, [_i, _i, _i, _i, _i, ctypes.POINTER(_i), ctypes.POINTER(_i)]),
     "fa_query_tensorcore_v3": (_i, [_i, ctypes.POINTER(TilingInfo)]),
     "fa_tensorcore_v3_hbm_bytes": (ctypes.c_double, [_i, _i, _i, _i, _i]),
     "fa_tensorcore_v3b_supported": (_i, [_i]),
@@ -198,6 +204,13 @@ def query_fused(head_dim: int, rows_per_block: int) -> dict:
     return info.as_dict()
 
 
+def query_fused_groups(head_dim: int, rows_per_block: int, kv_groups: int) -> dict:
+    info = TilingInfo()
+    _check(lib().fa_query_fused_groups(head_dim, rows_per_block, kv_groups, ctypes.byref(info)),
+           "fa_query_fused_groups")
+    return info.as_dict()
+
+
 def query_tensorcore_v3b(head_dim: int) -> dict:
     info = TilingInfo()
     _check(lib().fa_query_tensorcore_v3b(head_dim, ctypes.byref(info)), "fa_query_tensorcore_v3b")
@@ -218,6 +231,18 @@ def tensorcore_v3_rows_per_block(shape, causal: bool) -> int:
     """Query rows per workgroup the v3 entry runs at this shape (64, 128 or 256)."""
     s = _shape_of(shape)
     return int(lib().fa_tensorcore_v3_rows_per_block(s.batch, s.heads, s.seq_len, s.head_dim, int(causal)))
+
+
+def tensorcore_v3_config(shape, causal: bool):
+    """(rows per workgroup, KV wave groups) the v3 entry runs at this shape,
+    or None for an unsupported head_dim."""
+    s = _shape_of(shape)
+    rows, groups = ctypes.c_int(), ctypes.c_int()
+    st = lib().fa_tensorcore_v3_config(s.batch, s.heads, s.seq_len, s.head_dim, int(causal), ctypes.byref(rows),
+                                       ctypes.byref(groups))
+    if not _check(st, "fa_tensorcore_v3_config"):
+        return None
+    return rows.value, groups.value
 
 
 def get_last_error() -> int:
@@ -271,8 +296,8 @@ def launch_attention_unfused_profile(q, k, v, o, workspace, shape, causal: bool,
 
 
 def launch_attention_tensorcore_v3(q, k, v, o, shape, causal: bool, stream=None) -> bool:
-    """include/flash_attention.h:92 — the fused MFMA forward (128 query rows / workgroup;
-    64 when the 128-row grid has fewer workgroups than the device has CUs)."""
+    """include/flash_attention.h:92 — the fused MFMA forward in the workgroup
+    configuration tensorcore_v3_config(shape, causal) names."""
     s = _shape_of(shape)
     st = lib().fa_launch_attention_tensorcore_v3(_ptr(q), _ptr(k), _ptr(v), _ptr(o), s.batch, s.heads,
                                                  s.seq_len, s.head_dim, int(causal), _stream(stream))
@@ -287,6 +312,17 @@ def launch_attention_fused(q, k, v, o, shape, causal: bool, rows_per_block: int 
     st = lib().fa_launch_attention_fused(_ptr(q), _ptr(k), _ptr(v), _ptr(o), s.batch, s.heads, s.seq_len,
                                          s.head_dim, int(causal), int(rows_per_block), _stream(stream))
     return _check(st, "fa_launch_attention_fused")
+
+
+def launch_attention_fused_groups(q, k, v, o, shape, causal: bool, rows_per_block: int, kv_groups: int,
+                                  stream=None) -> bool:
+    """The fused forward in a pinned (rows per workgroup, KV groups)
+    configuration: (128, 2), (64, 2), (256, 1) or (64, 4) (head_dim 64)."""
+    s = _shape_of(shape)
+    st = lib().fa_launch_attention_fused_groups(_ptr(q), _ptr(k), _ptr(v), _ptr(o), s.batch, s.heads, s.seq_len,
+                                                s.head_dim, int(causal), int(rows_per_block), int(kv_groups),
+                                                _stream(stream))
+    return _check(st, "fa_launch_attention_fused_groups")
 
 
 def launch_attention_tensorcore_v3b(q, k, v, o, shape, causal: bool, stream=None) -> bool:
@@ -363,9 +399,10 @@ def attention_forward(q, k, v, causal: bool = False, kernel: str = "v3_mfma", ou
     elif kernel == "v3b_mfma":
         if not launch_attention_tensorcore_v3b(q, k, v, o, shape, causal):
             raise ValueError(f"head_dim {shape.head_dim} is not supported by the fused kernel")
-    elif kernel in ("v3_128", "v3_256"):
-        if not launch_attention_fused(q, k, v, o, shape, causal, rows_per_block=int(kernel[3:])):
-            raise ValueError(f"head_dim {shape.head_dim} is not supported by the fused kernel")
+    elif kernel in ("v3_128", "v3_256", "v3_64x4"):
+        rows, groups = FUSED_CONFIGS[kernel]
+        if not launch_attention_fused_groups(q, k, v, o, shape, causal, rows, groups):
+            raise ValueError(f"head_dim {shape.head_dim} is not supported by the {kernel} configuration")
     else:
         raise ValueError(f"unknown kernel {kernel!r}")
     return o

@@ -138,7 +138,7 @@ struct Cfg : TileCopy<D, kWpg>
     static constexpr int kQRowsPerIssue = 64 / (D / 8);                // rows one (64-lane) Q copy covers
     static constexpr int kQIssuesPerWave = kQIssues / kGroups;
     static_assert(D == 64 || D == 128, "head_dim 64 or 128");
-    static_assert(kGroups == 1 || kGroups == 2, "one or two wave groups");
+    static_assert(kGroups == 1 || kGroups == 2 || kGroups == 4, "one, two or four wave groups");
     static_assert(2 * kIssues < 64, "vmcnt range");
     static_assert(kQIssuesPerWave * kGroups == kQIssues, "Q copies split evenly over the waves");
     static_assert((kLdsElems + kQElems) * 2 <= 160 * 1024, "LDS of one workgroup");
@@ -541,7 +541,7 @@ __global__ __launch_bounds__(64 * kGroups * kWpg) void fused_attention_kernel(co
 
     const int last_key = kCausal ? min(last_row, n - 1) : n - 1;
     const int n_tiles = last_key / kTileKV + 1;
-    const fa::FusedSplit split = kGroups == 2 ? fa::fused_split(n_tiles) : fa::fused_single(n_tiles);
+    const fa::FusedSplit split = fa::fused_split_n(n_tiles, kGroups);
 
     // Tiles from t_mask on need the per-element mask (sequence tail, or this
     // wave's diagonal); tiles after t_last lie wholly above the diagonal.
@@ -569,8 +569,8 @@ __global__ __launch_bounds__(64 * kGroups * kWpg) void fused_attention_kernel(co
         // the array's base plus compile-time offsets.
         const uint32_t k_lds = lds_base + G * C::kGroupElems * 2;
         const uint32_t v_lds = k_lds + kStages * C::kTileElems * 2;
-        const int tb = G == 0 ? 0 : split.first1;                 // first tile of this group
-        const int cnt = G == 0 ? split.count0 : split.count1;
+        const int tb = split.first[G];                            // first tile of this group
+        const int cnt = split.count[G];
         const int lw = min(cnt - 1, t_last - tb);                 // last local tile this wave computes
         // First step whose "next" tile needs the per-element mask: the
         // diagonal / tail tile, or the dummy product after the wave's last
@@ -781,7 +781,7 @@ __global__ __launch_bounds__(64 * kGroups * kWpg) void fused_attention_kernel(co
             // 1 finishes (a per-step trace showed ~350 idle cycles per step
             // at head_dim 64; measured 1% per launch at head_dim 128, 2% at
             // 64).
-            constexpr bool kLeadB = G == 1 && !kCausal;
+            constexpr bool kLeadB = kGroups > 1 && G >= kGroups / 2 && !kCausal;
             if constexpr (kLeadB) __builtin_amdgcn_s_setprio(1);
             const bool rare = __any(tsum > kSumLimit);
             if (rare)
@@ -855,8 +855,19 @@ __global__ __launch_bounds__(64 * kGroups * kWpg) void fused_attention_kernel(co
     };
 
     if constexpr (kGroups == 1) run_group(std::integral_constant<int, 0>{});
-    else if (grp == 0) run_group(std::integral_constant<int, 0>{});
-    else run_group(std::integral_constant<int, 1>{});
+    else if constexpr (kGroups == 2)
+    {
+        if (grp == 0) run_group(std::integral_constant<int, 0>{});
+        else run_group(std::integral_constant<int, 1>{});
+    }
+    else
+    {
+        const int g4 = __builtin_amdgcn_readfirstlane(grp);
+        if (g4 == 0) run_group(std::integral_constant<int, 0>{});
+        else if (g4 == 1) run_group(std::integral_constant<int, 1>{});
+        else if (g4 == 2) run_group(std::integral_constant<int, 2>{});
+        else run_group(std::integral_constant<int, 3>{});
+    }
 
     // Normalise O^T blocks [kFirstDb, kFirstDb + kNumDb) of this wave's 32
     // rows by `inv` and store them (head dims 32*kFirstDb ..): O^T (lane =
@@ -968,8 +979,57 @@ __global__ __launch_bounds__(64 * kGroups * kWpg) void fused_attention_kernel(co
         store_rows(std::integral_constant<int, kKeep>{}, std::integral_constant<int, kHalfDb>{},
                    reinterpret_cast<uint16_t*>(x_recv), inv);
     };
+    if constexpr (kGroups == 4)
+    {
+        // Four groups: first groups 2 and 3 hand their whole partial (O^T,
+        // exponent base, partial row sums) to the group-0 / group-1 wave with
+        // the same slot, which folds it into its own (the same rescale as
+        // between steps); then groups 0 and 1 merge and store as above, and
+        // groups 2 and 3 only join that merge's barrier. The hand-over area
+        // lies past the one `finish` uses, in the free stage area.
+        constexpr int kFull = (D / 32) * 16 * 64;                     // one wave's O^T
+        constexpr int kSlotFloats = kFull + 128;
+        constexpr int kBase = kWpg * 2 * ((D / 64) * 16 * 64 + 128);  // past finish's area
+        static_assert(kBase + 2 * kWpg * kSlotFloats <= C::kLdsElems / 2, "hand-over area fits the stage area");
+        float* const area = reinterpret_cast<float*>(lds) + kBase + ((grp_s & 1) * kWpg + slot) * kSlotFloats;
+        if (grp_s >= 2)
+        {
+#pragma unroll
+            for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+                for (int r4 = 0; r4 < 4; ++r4)
+                {
+                    const f32x4 v4 = {f.o[db][4 * r4], f.o[db][4 * r4 + 1], f.o[db][4 * r4 + 2], f.o[db][4 * r4 + 3]};
+                    *reinterpret_cast<f32x4*>(area + ((db * 4 + r4) * 64 + lane) * 4) = v4;
+                }
+            area[kFull + lane] = rs.m;
+            area[kFull + 64 + lane] = rs.l;
+        }
+        wait_vm_lgkm0<0>();
+        barrier();
+        if (grp_s < 2)
+        {
+            const float m1 = area[kFull + lane];
+            const float l1 = area[kFull + 64 + lane];
+            const float m = __builtin_elementwise_maximum(rs.m, m1);
+            const float a0 = __builtin_amdgcn_exp2f(rs.m - m);
+            const float a1 = __builtin_amdgcn_exp2f(m1 - m);
+            rs.l = rs.l * a0 + l1 * a1;
+            rs.m = m;
+#pragma unroll
+            for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+                for (int r4 = 0; r4 < 4; ++r4)
+                {
+                    const f32x4 x = *reinterpret_cast<const f32x4*>(area + ((db * 4 + r4) * 64 + lane) * 4);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) f.o[db][4 * r4 + j] = f.o[db][4 * r4 + j] * a0 + x[j] * a1;
+                }
+        }
+    }
     if (grp_s == 0) finish(std::integral_constant<int, 0>{});
-    else finish(std::integral_constant<int, 1>{});
+    else if (grp_s == 1 || kGroups == 2) finish(std::integral_constant<int, 1>{});
+    else barrier();  // groups 2 and 3: the barrier inside finish
     }
 }
 
@@ -979,12 +1039,21 @@ const void* kernel_ptr()
     return reinterpret_cast<const void*>(&fused_attention_kernel<D, kWpg, kCausal, kGroups>);
 }
 
+// Whether a workgroup configuration exists for head_dim D: four KV groups
+// need four stage sets, which fit a CU's 160 KiB of LDS at head_dim 64 only.
+template <int kWpg, int kGroups>
+constexpr bool has_config(int head_dim)
+{
+    return head_dim == 64 || (head_dim == 128 && kGroups != 4);
+}
+
 template <int kWpg, int kGroups>
 const void* pick_kernel(int head_dim, bool causal)
 {
     if (head_dim == 64) return causal ? kernel_ptr<64, kWpg, true, kGroups>() : kernel_ptr<64, kWpg, false, kGroups>();
-    if (head_dim == 128)
-        return causal ? kernel_ptr<128, kWpg, true, kGroups>() : kernel_ptr<128, kWpg, false, kGroups>();
+    if constexpr (has_config<kWpg, kGroups>(128))
+        if (head_dim == 128)
+            return causal ? kernel_ptr<128, kWpg, true, kGroups>() : kernel_ptr<128, kWpg, false, kGroups>();
     return nullptr;
 }
 
@@ -1018,7 +1087,7 @@ template <int kWpg, int kGroups = 2>
 int launch_fused(const void* q, const void* k, const void* v, void* o, int batch, int heads, int seq_len,
                  int head_dim, int causal, void* stream_ptr)
 {
-    if (head_dim != 64 && head_dim != 128) return FA_ERROR_UNSUPPORTED;
+    if (!has_config<kWpg, kGroups>(head_dim)) return FA_ERROR_UNSUPPORTED;
     if (batch < 0 || heads < 0 || seq_len < 0) return hipErrorInvalidValue;
     const long long bh = static_cast<long long>(batch) * heads;
     if (bh == 0 || seq_len == 0) return hipSuccess;
@@ -1053,31 +1122,53 @@ int launch_fused(const void* q, const void* k, const void* v, void* o, int batch
     if (head_dim == 64)
         return causal ? launch_typed<64, kWpg, true, kGroups>(qb, kb, vb, ob, seq_len, qbk, tot, c_log2, paired, stream)
                       : launch_typed<64, kWpg, false, kGroups>(qb, kb, vb, ob, seq_len, qbk, tot, c_log2, 0, stream);
-    return causal ? launch_typed<128, kWpg, true, kGroups>(qb, kb, vb, ob, seq_len, qbk, tot, c_log2, paired, stream)
-                  : launch_typed<128, kWpg, false, kGroups>(qb, kb, vb, ob, seq_len, qbk, tot, c_log2, 0, stream);
+    if constexpr (has_config<kWpg, kGroups>(128))
+        return causal ? launch_typed<128, kWpg, true, kGroups>(qb, kb, vb, ob, seq_len, qbk, tot, c_log2, paired, stream)
+                      : launch_typed<128, kWpg, false, kGroups>(qb, kb, vb, ob, seq_len, qbk, tot, c_log2, 0, stream);
+    return FA_ERROR_UNSUPPORTED;
 }
 
-// Rows per workgroup the v3 entry point uses for a shape (measured on
-// MI355X):
-//   * 64 when the 128-row grid has fewer workgroups than CUs (small
-//     batch*heads*seq_len): twice as many workgroups finish sooner;
-//   * 256 (one wave group) when even 256-row workgroups give every CU one
-//     (dense), or, causal, for seq_len >= 8192 with at least two rounds of
-//     them: half the L2->LDS copies per score and no merge, 2-7% faster
-//     there; shorter causal sequences lose more to the coarser diagonal
-//     blocks than they gain;
-//   * 128 otherwise.
-// Dense outputs of the 64- and 128-row configurations are bitwise identical
-// (each wave computes its 32 rows the same way in both).
-int auto_rows_per_block(int batch, int heads, int seq_len, int causal)
+// The workgroup configuration (query rows, KV wave groups) the v3 entry
+// point uses for a shape, from measurements on MI355X (back-to-back
+// launches, medians of repeated runs):
+//   * fewer 128-row workgroups than CUs (small batch*heads*seq_len): 64 rows,
+//     so twice as many workgroups finish sooner; at head_dim 64 with
+//     seq_len >= 1024 split over four KV groups of two waves (every SIMD
+//     keeps two waves: (1,8,2048,64) 14.5 -> 12.9 us), else two groups;
+//   * head_dim 128: 256 rows in one group when even 256-row workgroups give
+//     every CU one (dense), or, causal, for seq_len >= 8192 with at least two
+//     rounds of them: half the L2->LDS copies per score and no merge, 2-7%
+//     faster there; shorter causal sequences lose more to the coarser
+//     diagonal blocks than they gain;
+//   * head_dim 64, causal, more than one round of 128-row workgroups and
+//     seq_len <= 2048: 64 rows in two groups, two workgroups resident per CU
+//     (80 KiB of LDS each), whose prologues and epilogues overlap the other's
+//     steps ((4,8,2048,64) causal 33.7 -> 28.7 us);
+//   * otherwise 128 rows in two groups (head_dim 64 never gains from 256
+//     rows: 1-4 % slower on every grid measured).
+// Dense outputs of the 64- and 128-row two-group configurations are bitwise
+// identical (each wave computes its 32 rows the same way in both).
+struct FusedConfig
 {
-    if (batch <= 0 || heads <= 0 || seq_len <= 0) return 128;
+    int rows;
+    int groups;
+};
+
+FusedConfig auto_config(int batch, int heads, int seq_len, int head_dim, int causal)
+{
+    if (batch <= 0 || heads <= 0 || seq_len <= 0) return {128, 2};
     const long long bh = static_cast<long long>(batch) * heads;
     const long long cus = device_compute_units();
-    if (bh * ((static_cast<long long>(seq_len) + 127) / 128) < cus) return 64;
-    const long long wide = bh * ((static_cast<long long>(seq_len) + 255) / 256);
-    if (causal ? (seq_len >= 8192 && wide >= 2 * cus) : wide >= cus) return 256;
-    return 128;
+    const long long blocks128 = bh * ((static_cast<long long>(seq_len) + 127) / 128);
+    if (blocks128 < cus) return (head_dim == 64 && seq_len >= 1024) ? FusedConfig{64, 4} : FusedConfig{64, 2};
+    if (head_dim == 128)
+    {
+        const long long wide = bh * ((static_cast<long long>(seq_len) + 255) / 256);
+        if (causal ? (seq_len >= 8192 && wide >= 2 * cus) : wide >= cus) return {256, 1};
+        return {128, 2};
+    }
+    if (causal && blocks128 > cus && seq_len <= 2048) return {64, 2};
+    return {128, 2};
 }
 
 template <int kWpg, int kGroups = 2>
@@ -1090,6 +1181,7 @@ int query_fused(int head_dim, fa_tiling_info* info)
     info->supported = 1;
     info->block_size = 64 * kGroups * kWpg;
     info->waves_per_block = kGroups * kWpg;
+    info->kv_groups = kGroups;
     info->tile_kv = kTileKV;
     info->rows_per_block = 32 * kWpg;
 
@@ -1156,22 +1248,52 @@ extern "C" {
 
 int fa_tensorcore_v3_supported(int head_dim) { return head_dim == 64 || head_dim == 128; }
 
+int fa_tensorcore_v3_config(int batch, int heads, int seq_len, int head_dim, int causal, int* rows_per_block,
+                            int* kv_groups)
+{
+    if (!rows_per_block || !kv_groups) return fa::record_status(hipErrorInvalidValue);
+    *rows_per_block = *kv_groups = 0;
+    if (head_dim != 64 && head_dim != 128) return FA_ERROR_UNSUPPORTED;
+    const FusedConfig c = auto_config(batch, heads, seq_len, head_dim, causal);
+    *rows_per_block = c.rows;
+    *kv_groups = c.groups;
+    return hipSuccess;
+}
+
 int fa_tensorcore_v3_rows_per_block(int batch, int heads, int seq_len, int head_dim, int causal)
 {
     if (head_dim != 64 && head_dim != 128) return 0;
-    return auto_rows_per_block(batch, heads, seq_len, causal);
+    return auto_config(batch, heads, seq_len, head_dim, causal).rows;
+}
+
+int fa_launch_attention_fused_groups(const void* q, const void* k, const void* v, void* o, int batch, int heads,
+                                     int seq_len, int head_dim, int causal, int rows_per_block, int kv_groups,
+                                     void* stream)
+{
+    int status = hipErrorInvalidValue;
+    if (rows_per_block == 128 && kv_groups == 2)
+        status = launch_fused<4>(q, k, v, o, batch, heads, seq_len, head_dim, causal, stream);
+    else if (rows_per_block == 64 && kv_groups == 2)
+        status = launch_fused<2>(q, k, v, o, batch, heads, seq_len, head_dim, causal, stream);
+    else if (rows_per_block == 256 && kv_groups == 1)
+        status = launch_fused<8, 1>(q, k, v, o, batch, heads, seq_len, head_dim, causal, stream);
+    else if (rows_per_block == 64 && kv_groups == 4)
+        status = launch_fused<2, 4>(q, k, v, o, batch, heads, seq_len, head_dim, causal, stream);
+    return fa::record_status(status);
 }
 
 int fa_launch_attention_fused(const void* q, const void* k, const void* v, void* o, int batch, int heads,
                               int seq_len, int head_dim, int causal, int rows_per_block, void* stream)
 {
-    if (rows_per_block == 0) rows_per_block = auto_rows_per_block(batch, heads, seq_len, causal);
-    int status = hipErrorInvalidValue;
-    if (rows_per_block == 128) status = launch_fused<4>(q, k, v, o, batch, heads, seq_len, head_dim, causal, stream);
-    else if (rows_per_block == 64) status = launch_fused<2>(q, k, v, o, batch, heads, seq_len, head_dim, causal, stream);
-    else if (rows_per_block == 256)
-        status = launch_fused<8, 1>(q, k, v, o, batch, heads, seq_len, head_dim, causal, stream);
-    return fa::record_status(status);
+    int groups = rows_per_block == 256 ? 1 : 2;
+    if (rows_per_block == 0)
+    {
+        const FusedConfig c = auto_config(batch, heads, seq_len, head_dim, causal);
+        rows_per_block = c.rows;
+        groups = c.groups;
+    }
+    return fa_launch_attention_fused_groups(q, k, v, o, batch, heads, seq_len, head_dim, causal, rows_per_block,
+                                            groups, stream);
 }
 
 int fa_launch_attention_tensorcore_v3(const void* q, const void* k, const void* v, void* o, int batch, int heads,
@@ -1182,13 +1304,19 @@ int fa_launch_attention_tensorcore_v3(const void* q, const void* k, const void* 
 
 int fa_query_tensorcore_v3(int head_dim, fa_tiling_info* info) { return fa::record_status(query_fused<4>(head_dim, info)); }
 
-int fa_query_fused(int head_dim, int rows_per_block, fa_tiling_info* info)
+int fa_query_fused_groups(int head_dim, int rows_per_block, int kv_groups, fa_tiling_info* info)
 {
     int status = hipErrorInvalidValue;
-    if (rows_per_block == 128) status = query_fused<4>(head_dim, info);
-    else if (rows_per_block == 64) status = query_fused<2>(head_dim, info);
-    else if (rows_per_block == 256) status = query_fused<8, 1>(head_dim, info);
+    if (rows_per_block == 128 && kv_groups == 2) status = query_fused<4>(head_dim, info);
+    else if (rows_per_block == 64 && kv_groups == 2) status = query_fused<2>(head_dim, info);
+    else if (rows_per_block == 256 && kv_groups == 1) status = query_fused<8, 1>(head_dim, info);
+    else if (rows_per_block == 64 && kv_groups == 4) status = query_fused<2, 4>(head_dim, info);
     return fa::record_status(status);
+}
+
+int fa_query_fused(int head_dim, int rows_per_block, fa_tiling_info* info)
+{
+    return fa_query_fused_groups(head_dim, rows_per_block, rows_per_block == 256 ? 1 : 2, info);
 }
 
 // The model for the configuration the v3 entry runs at this shape (64, 128
@@ -1196,7 +1324,7 @@ int fa_query_fused(int head_dim, int rows_per_block, fa_tiling_info* info)
 double fa_tensorcore_v3_hbm_bytes(int batch, int heads, int seq_len, int head_dim, int causal)
 {
     return blocked_hbm_bytes(batch, heads, seq_len, head_dim, causal,
-                             auto_rows_per_block(batch, heads, seq_len, causal));
+                             auto_config(batch, heads, seq_len, head_dim, causal).rows);
 }
 
 int fa_tensorcore_v3b_supported(int head_dim) { return head_dim == 64 || head_dim == 128; }

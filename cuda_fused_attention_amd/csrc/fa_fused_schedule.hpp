@@ -35,12 +35,14 @@ constexpr int kFusedStages = 4;   // LDS stages per tensor (K, V) per wave group
 constexpr int kFusedKAhead = kFusedStages;      // into K_jj's stage (read in step jj - 2)
 constexpr int kFusedVAhead = kFusedStages - 1;  // into V_{jj-1}'s stage (read in step jj - 1)
 
+constexpr int kFusedMaxGroups = 4;  // wave groups (KV streams) per workgroup: 1, 2 or 4
+
 struct FusedSplit
 {
-    int count0;    // KV tiles walked by group 0: [0, count0)
-    int first1;    // first tile of group 1
-    int count1;    // KV tiles walked by group 1: [first1, first1 + count1)
-    int barriers;  // barriers each group executes before the merge
+    int groups;                  // wave groups sharing the KV range
+    int first[kFusedMaxGroups];  // first tile walked by group g
+    int count[kFusedMaxGroups];  // KV tiles walked by group g: [first[g], first[g] + count[g])
+    int barriers;                // barriers each group executes before the merge
 };
 
 // Barriers group `g` executes for `count` tiles: one after the prologue DMAs,
@@ -74,28 +76,30 @@ FA_HD inline void fused_group_walk(int count, Step&& step)
     }
 }
 
-FA_HD inline FusedSplit fused_split(int n_tiles)
+// The KV range of n_tiles tiles split over `groups` wave groups in order:
+// contiguous ranges, the earlier groups one tile longer when the count does
+// not divide evenly. Every group pads to the longest group's barrier count.
+FA_HD inline FusedSplit fused_split_n(int n_tiles, int groups)
 {
     FusedSplit s;
-    s.count0 = (n_tiles + 1) / 2;
-    s.first1 = s.count0;
-    s.count1 = n_tiles - s.count0;
-    const int b0 = fused_group_barriers(0, s.count0);
-    const int b1 = fused_group_barriers(1, s.count1);
-    s.barriers = b0 > b1 ? b0 : b1;
+    s.groups = groups;
+    const int base = n_tiles / groups;
+    const int rem = n_tiles % groups;
+    int first = 0;
+    for (int g = 0; g < kFusedMaxGroups; ++g)
+    {
+        s.count[g] = g < groups ? base + (g < rem ? 1 : 0) : 0;
+        s.first[g] = first;
+        first += s.count[g];
+    }
+    s.barriers = fused_group_barriers(0, s.count[0]);
     return s;
 }
 
-// The same walk for a workgroup with one wave group (no split of the KV
-// range): group 0 takes every tile.
-FA_HD inline FusedSplit fused_single(int n_tiles)
-{
-    FusedSplit s;
-    s.count0 = n_tiles;
-    s.first1 = n_tiles;
-    s.count1 = 0;
-    s.barriers = fused_group_barriers(0, n_tiles);
-    return s;
-}
+// Two groups: group 0 walks the first half of the KV tiles, group 1 the rest.
+FA_HD inline FusedSplit fused_split(int n_tiles) { return fused_split_n(n_tiles, 2); }
+
+// One wave group (no split of the KV range): group 0 takes every tile.
+FA_HD inline FusedSplit fused_single(int n_tiles) { return fused_split_n(n_tiles, 1); }
 
 }  // namespace fa

@@ -64,6 +64,7 @@ typedef struct fa_tiling_info {
                                         compiler's report; -1 if unknown */
     int waves_per_block;             /* wave64 count per workgroup (MI355X) */
     int compute_units;               /* CUs on the current device (MI355X) */
+    int kv_groups;                   /* wave groups splitting the KV range (MI355X) */
 } fa_tiling_info;
 
 /* No counterpart in the reference (its launchers return void and leave
@@ -147,15 +148,32 @@ int fa_launch_attention_fused(const void* q, const void* k, const void* v, void*
                               int batch, int heads, int seq_len, int head_dim,
                               int causal, int rows_per_block, void* stream);
 
+/* No counterpart in the reference: the fused forward in any of its workgroup
+ * configurations, named by query rows per workgroup and the number of wave
+ * groups that split the KV range: (128, 2) is v3's default, (64, 2) v3b,
+ * (256, 1) one group of 8 waves, (64, 4) four groups of 2 waves (head_dim 64
+ * only: FA_ERROR_UNSUPPORTED at 128, whose four stage sets would not fit
+ * LDS). Other pairs return hipErrorInvalidValue. */
+int fa_launch_attention_fused_groups(const void* q, const void* k, const void* v, void* o,
+                                     int batch, int heads, int seq_len, int head_dim,
+                                     int causal, int rows_per_block, int kv_groups, void* stream);
+
 /* No counterpart in the reference: fa_query_tensorcore_v3 for the
  * configuration fa_launch_attention_fused runs with rows_per_block (64, 128
- * or 256). agprs_per_thread comes from the compiler's resource report of
+ * or 256), or fa_launch_attention_fused_groups with (rows_per_block,
+ * kv_groups). agprs_per_thread comes from the compiler's resource report of
  * the kernel, recorded when the library was built. */
 int fa_query_fused(int head_dim, int rows_per_block, fa_tiling_info* info);
+int fa_query_fused_groups(int head_dim, int rows_per_block, int kv_groups, fa_tiling_info* info);
 
 /* No counterpart in the reference (whose v3 has one configuration): the
- * query rows per workgroup (64, 128 or 256) fa_launch_attention_tensorcore_v3
- * runs at this shape on the current device; 0 for an unsupported head_dim. */
+ * workgroup configuration fa_launch_attention_tensorcore_v3 runs at this
+ * shape on the current device, as (query rows per workgroup, KV wave groups):
+ * (64, 2), (64, 4), (128, 2) or (256, 1). FA_ERROR_UNSUPPORTED (both set to
+ * 0) for an unsupported head_dim. fa_tensorcore_v3_rows_per_block returns the
+ * rows alone (0 for an unsupported head_dim). */
+int fa_tensorcore_v3_config(int batch, int heads, int seq_len, int head_dim, int causal,
+                            int* rows_per_block, int* kv_groups);
 int fa_tensorcore_v3_rows_per_block(int batch, int heads, int seq_len, int head_dim, int causal);
 
 /* include/flash_attention.h:94, kernels/v3/v3_tensorcore.cu:752-790 — the
@@ -184,7 +202,8 @@ double fa_tensorcore_v3b_hbm_bytes(int batch, int heads, int seq_len, int head_d
 /* Harness support (benchmarks/bench_flash_attention.cu:265-299): run
  * `warmup` untimed launches of kernel `which` (0 = unfused, 1 = v3 fused,
  * 2 = v3b fused, 3 = fused with 128 rows per workgroup whatever the shape,
- * 4 = fused with 256 rows per workgroup),
+ * 4 = fused with 256 rows per workgroup, 5 = fused with 64 rows and four
+ * KV groups),
  * synchronise, then `iters` launches each bracketed by
  * hipEventRecord on `stream`; elapsed milliseconds go to samples_ms[iters].
  * Returns FA_ERROR_UNSUPPORTED for an unsupported head_dim and

@@ -405,15 +405,20 @@ int main(int argc, char** argv)
     // Every workgroup configuration of the MFMA kernel (v3 picks one per
     // shape; the "v3 rows" column of the grid below says which), with the
     // AGPRs of the compiler's resource report.
-    std::printf("\nMFMA kernel configurations (fa_query_fused):\n  %8s %8s %6s %6s %6s %6s %12s %10s\n", "q_rows",
-                "head_dim", "waves", "block", "VGPRs", "AGPRs", "shared/block", "blocks/CU");
-    for (int rows : {64, 128, 256})
+    std::printf("\nMFMA kernel configurations (fa_query_fused_groups):\n  %8s %9s %8s %6s %6s %6s %6s %12s %10s\n",
+                "q_rows", "kv_groups", "head_dim", "waves", "block", "VGPRs", "AGPRs", "shared/block", "blocks/CU");
+    for (const auto& [rows, groups] : {std::pair{64, 2}, std::pair{64, 4}, std::pair{128, 2}, std::pair{256, 1}})
         for (int d : {64, 128})
         {
             fa_tiling_info info{};
-            if (fa_query_fused(d, rows, &info) != 0) return 2;
-            std::printf("  %8d %8d %6d %6d %6d %6d %11dB %10d\n", rows, d, info.waves_per_block, info.block_size,
-                        info.registers_per_thread, info.agprs_per_thread, info.shared_bytes_per_block,
+            if (fa_query_fused_groups(d, rows, groups, &info) != 0) return 2;
+            if (!info.supported)
+            {
+                std::printf("  %8d %9d %8d  (no configuration)\n", rows, groups, d);
+                continue;
+            }
+            std::printf("  %8d %9d %8d %6d %6d %6d %6d %11dB %10d\n", rows, groups, d, info.waves_per_block,
+                        info.block_size, info.registers_per_thread, info.agprs_per_thread, info.shared_bytes_per_block,
                         info.max_blocks_per_sm);
         }
     std::printf("\n");
@@ -500,9 +505,11 @@ int main(int argc, char** argv)
                     const Problem p{q.bf16(), k.bf16(), v.bf16(), o.bf16(), static_cast<float*>(ws), s, causal};
                     // 4*B*H*N^2*D, halved for causal (BASELINE's convention)
                     const double flops = 4.0 * b * s.heads * static_cast<double>(nlen) * nlen * d * (causal ? 0.5 : 1.0);
-                    std::printf("B=%d H=8 N=%d D=%d %s (v3 rows per workgroup: %d)\n  %-16s %10s %10s %9s %9s %9s\n",
-                                b, nlen, d, causal ? "causal" : "dense",
-                                fa_tensorcore_v3_rows_per_block(b, 8, nlen, d, causal ? 1 : 0), "kernel", "median ms",
+                    int cfg_rows = 0, cfg_groups = 0;
+                    (void)fa_tensorcore_v3_config(b, 8, nlen, d, causal ? 1 : 0, &cfg_rows, &cfg_groups);
+                    std::printf("B=%d H=8 N=%d D=%d %s (v3: %d rows per workgroup, %d KV groups)\n"
+                                "  %-16s %10s %10s %9s %9s %9s\n",
+                                b, nlen, d, causal ? "causal" : "dense", cfg_rows, cfg_groups, "kernel", "median ms",
                                 "IQR ms", "TFLOPS", "HBM GB", "speedup");
                     double baseline_ms = 0.0;
                     for (const Entry& e : table)

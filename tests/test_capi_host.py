@@ -56,6 +56,8 @@ def test_host_models_match_oracle(fa_lib, oracle_mod):
             # the model follows the configuration the v3 entry runs at this shape
             rows = fa_lib.tensorcore_v3_rows_per_block(shape, causal)
             assert rows in (64, 128, 256)
+            assert fa_lib.tensorcore_v3_config(shape, causal) in ((64, 2), (64, 4), (128, 2), (256, 1))
+            assert fa_lib.tensorcore_v3_config(shape, causal)[0] == rows
             assert fa_lib.tensorcore_v3_hbm_bytes(shape, causal) == L.fa_oracle_blocked_kv_hbm_bytes(B, H, N, D, int(causal), rows, 32)
             assert fa_lib.tensorcore_v3b_hbm_bytes(shape, causal) == L.fa_oracle_blocked_kv_hbm_bytes(B, H, N, D, int(causal), 64, 32)
         assert fa_lib.unfused_workspace_bytes(shape) == L.fa_oracle_unfused_workspace_bytes(B, H, N)
@@ -82,6 +84,23 @@ def test_error_state_records_host_side_rejections(fa_lib):
     assert L.fa_launch_softmax_rows_inplace(None, 3, 10, None) == 1
     assert L.fa_query_fused(64, 96, None) == 1
     assert fa_lib.get_last_error() == 1 and fa_lib.get_last_error() == 0
+
+
+def test_configuration_rule_without_a_device(fa_lib):
+    """The v3 configuration rule on the CPU (the CU count falls back to an
+    MI355X's 256): the four (2,8,2048,D) metric shapes run 128 rows in two
+    groups; small head_dim-64 grids take four KV groups; an unsupported
+    head_dim reports no configuration."""
+    for d in (64, 128):
+        for causal in (False, True):
+            assert fa_lib.tensorcore_v3_config((2, 8, 2048, d), causal) == (128, 2)
+    assert fa_lib.tensorcore_v3_config((1, 8, 2048, 64), True) == (64, 4)
+    assert fa_lib.tensorcore_v3_config((1, 8, 512, 64), False) == (64, 2)
+    assert fa_lib.tensorcore_v3_config((4, 8, 8192, 64), False) == (128, 2)
+    assert fa_lib.tensorcore_v3_config((4, 8, 8192, 128), False) == (256, 1)
+    assert fa_lib.tensorcore_v3_config((4, 8, 2048, 64), True) == (64, 2)
+    assert fa_lib.tensorcore_v3_config((1, 8, 512, 96), False) is None
+    assert fa_lib.tensorcore_v3_rows_per_block((1, 8, 512, 96), False) == 0
 
 
 def test_supported_head_dims(fa_lib):

@@ -1,17 +1,17 @@
 """CPU check of the fused kernel's tile / stage / barrier schedule
 (csrc/fa_fused_schedule.hpp).
 
-The kernel's two wave groups must execute exactly the same number of
-workgroup barriers or the workgroup deadlocks, and the LDS stage rotation must
+The kernel's wave groups (one, two or four) must execute exactly the same
+number of workgroup barriers or the workgroup deadlocks, and the LDS stage rotation must
 never overwrite a tile that a later step still reads. The header holds the
 walk the kernel itself runs (fused_group_walk) and the pipeline distances; this
 test compiles it with g++, replays the walk with a model of the kernel's
 per-step actions and checks, for every tile count:
   (a) the walk performs fused_group_barriers() barriers and the compile-time
       step argument equals jj % kFusedUnroll;
-  (b) both groups reach the same total, split.barriers, after padding (the
-      groups run in phase: every step of either group has one workgroup
-      barrier);
+  (b) every group reaches the same total, split.barriers, after padding (the
+      groups run in phase: every step of any group has one workgroup
+      barrier), and the groups' tile ranges tile [0, n_tiles) in order;
   (c) every K / V stage is read only after the DMA that filled it was waited
       for (the model's waits are the kernel's vmcnt waits: all copy groups but
       the last n issued have landed) and a barrier passed, and no DMA targets
@@ -63,11 +63,20 @@ void read(std::vector<Stage>& arr, int st, int tile) {
 }
 
 int main() {
+    for (int n_groups : {1, 2, 4})
     for (int n_tiles = 1; n_tiles <= 3000; ++n_tiles) {
-        const FusedSplit sp = fused_split(n_tiles);
-        if (sp.count0 + sp.count1 != n_tiles || sp.count0 < sp.count1 || sp.first1 != sp.count0) ++bad;
-        for (int g = 0; g < 2; ++g) {
-            const int cnt = g == 0 ? sp.count0 : sp.count1;
+        const FusedSplit sp = n_groups == 2 ? fused_split(n_tiles) : n_groups == 1 ? fused_single(n_tiles)
+                                                                                   : fused_split_n(n_tiles, 4);
+        if (sp.groups != n_groups) ++bad;
+        int next = 0;
+        for (int g = 0; g < kFusedMaxGroups; ++g) {
+            if (g >= n_groups) { if (sp.count[g] != 0) ++bad; continue; }
+            if (sp.first[g] != next || sp.count[g] > sp.count[0] || sp.count[g] < sp.count[0] - 1) ++bad;
+            next += sp.count[g];
+        }
+        if (next != n_tiles) ++bad;
+        for (int g = 0; g < n_groups; ++g) {
+            const int cnt = sp.count[g];
             ks.assign(S, Stage{}); vs.assign(S, Stage{}); epoch = 0; groups = 0;
             // prologue: K_0 .. K_{S-1}, V_0 .. V_{S-2}
             for (int x = 0; x < S; ++x) dma(ks, x, x, -1);

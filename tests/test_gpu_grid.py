@@ -15,7 +15,7 @@ test also asserts that the inputs do reach |s| > 50.
 import numpy as np
 import pytest
 
-from gpu_common import HOST_THREADS, KERNELS, from_dev, run, say, to_dev
+from gpu_common import HOST_THREADS, from_dev, kernels_for, run, say, to_dev
 
 pytestmark = [pytest.mark.gpu, pytest.mark.slow]
 
@@ -47,7 +47,7 @@ def test_grid_tolerance(fa, oracle_mod, B, D):
         qb, kb, vb = oracle_mod.make_inputs(B, H, N, D, seeds=grid_seeds(B, N, D))
         ref = oracle_mod.attention(qb, kb, vb, causal, threads=HOST_THREADS).reshape(-1, D)
         q, k, v = to_dev(qb), to_dev(kb), to_dev(vb)
-        for kernel in KERNELS:
+        for kernel in kernels_for(D):
             say("grid", kernel, B, H, N, D, causal)
             out = from_dev(run(fa, kernel, q, k, v, causal)).reshape(-1, D)
             # every element of the output must be finite (NaN prefill)
@@ -84,7 +84,7 @@ def test_long_sequence_stress(fa, oracle_mod):
     assert row_max.max() > 50, row_max.max()
     ref = oracle_mod.attention(qb, kb, vb, True, threads=HOST_THREADS).reshape(-1, D)
     q, k, v = to_dev(qb), to_dev(kb), to_dev(vb)
-    for kernel in KERNELS:
+    for kernel in kernels_for(D):
         say("stress", kernel)
         out = from_dev(run(fa, kernel, q, k, v, True)).reshape(-1, D)
         assert int(np.count_nonzero((out & 0x7F80) == 0x7F80)) == 0

@@ -16,7 +16,8 @@ import os
 import numpy as np
 import pytest
 
-from gpu_common import HOST_THREADS, KERNELS, from_dev, nan_like, run, run_bits, say, to_dev
+from gpu_common import (FUSED_KERNELS, HOST_THREADS, KERNELS, from_dev, kernels_for, nan_like, run, run_bits, say,
+                        supports, to_dev)
 
 pytestmark = pytest.mark.gpu
 HERE = os.path.dirname(os.path.abspath(__file__))
@@ -63,6 +64,8 @@ def test_golden_fixture(fa, oracle_mod, kernel):
 @pytest.mark.parametrize("causal", [False, True])
 def test_reference_accuracy_shapes(fa, oracle_mod, kernel, head_dim, causal):
     """The reference's accuracy suite: (1,2,256,D), its own mt19937 normal inputs."""
+    if not supports(kernel, head_dim):
+        pytest.skip(f"{kernel} has no head_dim {head_dim} configuration")
     q, k, v = oracle_mod.make_inputs(1, 2, 256, head_dim, "normal_mt19937")
     ref = oracle_mod.attention(q, k, v, causal)
     say("refacc", kernel, head_dim, causal)
@@ -81,6 +84,8 @@ def test_boundary_matrix(fa, oracle_mod, kernel, family):
     fails = []
     for n in BOUNDARY_N:
         for d in (64, 128):
+            if not supports(kernel, d):
+                continue
             q, k, v = oracle_mod.make_inputs(1, 2, n, d, family)
             for causal in (False, True):
                 ref = oracle_mod.attention(q, k, v, causal, threads=HOST_THREADS)
@@ -97,7 +102,7 @@ def test_multi_slab_ragged(fa, oracle_mod):
         q, k, v = oracle_mod.make_inputs(B, H, N, D, seeds={"q": 5, "k": 6, "v": 7})
         for causal in (False, True):
             ref = oracle_mod.attention(q, k, v, causal, threads=HOST_THREADS)
-            for kernel in KERNELS:
+            for kernel in kernels_for(D):
                 say("ragged", kernel, B, H, N, D, causal)
                 check(oracle_mod, run_bits(fa, kernel, q, k, v, causal), ref, f"ragged {kernel} {(B, H, N, D, causal)}")
 
@@ -116,7 +121,7 @@ def test_causal_work_layouts(fa, oracle_mod):
     for (B, H, N, D) in cases:
         q, k, v = oracle_mod.make_inputs(B, H, N, D, seeds={"q": 41, "k": 42, "v": 43})
         ref = oracle_mod.attention(q, k, v, True, threads=HOST_THREADS)
-        for kernel in ("v3_mfma", "v3b_mfma", "v3_128", "v3_256"):
+        for kernel in kernels_for(D, FUSED_KERNELS):
             say("causal layout", kernel, B, H, N, D)
             check(oracle_mod, run_bits(fa, kernel, q, k, v, True), ref, f"causal layout {kernel} {(B, H, N, D)}")
 
@@ -153,7 +158,7 @@ def test_base_moves(fa, oracle_mod):
             for name, qq, kk, vv in cases:
                 for causal in (False, True):
                     ref = oracle_mod.attention(qq, kk, vv, causal, threads=HOST_THREADS)
-                    for kernel in ("v3_mfma", "v3b_mfma", "v3_128", "v3_256"):
+                    for kernel in kernels_for(D, FUSED_KERNELS):
                         say("base moves", name, kernel, N, D, causal)
                         check(oracle_mod, run_bits(fa, kernel, qq, kk, vv, causal), ref,
                               f"base moves {name} {kernel} {(N, D, causal)}")
@@ -187,27 +192,35 @@ def test_v3_and_v3b_agree(fa, oracle_mod):
 
 
 def test_v3_picks_the_configuration_by_grid(fa, oracle_mod):
-    """The v3 entry runs 64 rows per workgroup when the 128-row grid has fewer
-    workgroups than the device has CUs; 256 (one wave group) when even
-    256-row workgroups give every CU one (dense) or, causal, for seq_len >=
-    8192 with two rounds of them; else 128. Its output equals the
-    pinned configuration's bit for bit on each side of each threshold."""
+    """The v3 entry's configuration rule: 64 rows per workgroup when the
+    128-row grid has fewer workgroups than the device has CUs (four KV groups
+    at head_dim 64 with seq_len >= 1024, else two); at head_dim 128, 256 rows
+    in one group when even 256-row workgroups give every CU one (dense) or,
+    causal, for seq_len >= 8192 with two rounds of them; at head_dim 64,
+    causal, more than one round and seq_len <= 2048, 64 rows in two groups;
+    else 128 rows in two groups. Its output equals the pinned configuration's
+    bit for bit on each side of each threshold."""
     cus = fa.query_tensorcore_v3(64)["compute_units"]
     assert cus > 0
     cases = [
-        ((1, 2, 700, 64), (False, True), "v3b_mfma"),           # 12 workgroups of 128 rows
+        ((1, 2, 700, 64), (False, True), "v3b_mfma"),           # 12 workgroups of 128 rows, seq_len < 1024
+        ((1, 4, 1024, 64), (False, True), "v3_64x4"),           # 32 workgroups of 128 rows, head_dim 64
+        ((1, 4, 1024, 128), (False, True), "v3b_mfma"),         # the same at head_dim 128
         ((1, cus // 2, 256, 64), (False, True), "v3_128"),      # `cus` of 128 rows, head_dim 64
         ((1, cus // 2, 256, 128), (False, True), "v3_128"),     # `cus` of 128 rows, `cus`/2 of 256
         ((1, cus, 256, 128), (False,), "v3_256"),               # `cus` workgroups of 256 rows, dense
-        ((1, cus, 256, 64), (False,), "v3_256"),
+        ((1, cus, 256, 64), (False,), "v3_128"),                # head_dim 64: never 256 rows
+        ((1, cus // 8, 2048, 64), (True,), "v3b_mfma"),         # head_dim 64 causal, 2 rounds, seq_len 2048
+        ((1, cus // 16, 4096, 64), (True,), "v3_128"),          # ... and seq_len 4096
         ((1, 2 * cus // 32, 8192, 128), (True,), "v3_256"),     # causal, 2 * `cus` of 256 rows
         ((1, 4 * cus // 16, 4096, 128), (True,), "v3_128"),     # causal below 8192 keys
     ]
-    rows_of = {"v3b_mfma": 64, "v3_128": 128, "v3_256": 256}
     for (B, H, N, D), masks, pinned in cases:
         q, k, v = (to_dev(x) for x in oracle_mod.make_inputs(B, H, N, D))
         for causal in masks:
-            assert fa.tensorcore_v3_rows_per_block(fa.AttentionShape(B, H, N, D), causal) == rows_of[pinned]
+            shape = fa.AttentionShape(B, H, N, D)
+            assert fa.tensorcore_v3_config(shape, causal) == fa.FUSED_CONFIGS[pinned], (shape, causal, pinned)
+            assert fa.tensorcore_v3_rows_per_block(shape, causal) == fa.FUSED_CONFIGS[pinned][0]
             say("v3 dispatch", B, H, N, D, causal, pinned)
             a = from_dev(run(fa, "v3_mfma", q, k, v, causal))
             b = from_dev(run(fa, pinned, q, k, v, causal))
@@ -216,7 +229,7 @@ def test_v3_picks_the_configuration_by_grid(fa, oracle_mod):
 
 def test_deterministic(fa, oracle_mod):
     q, k, v = (to_dev(x) for x in oracle_mod.make_inputs(2, 4, 1000, 128))
-    for kernel in KERNELS:
+    for kernel in kernels_for(128):
         for causal in (False, True):
             say("determinism", kernel, causal)
             a = from_dev(run(fa, kernel, q, k, v, causal))
@@ -232,7 +245,7 @@ def test_non_default_stream(fa, oracle_mod):
     s = torch.cuda.Stream()
     qd, kd, vd = to_dev(q), to_dev(k), to_dev(v)
     torch.cuda.synchronize()
-    for kernel in KERNELS:
+    for kernel in kernels_for(128):
         say("stream", kernel)
         with torch.cuda.stream(s):
             o = run(fa, kernel, qd, kd, vd, True, stream=s)
