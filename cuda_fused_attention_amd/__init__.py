@@ -34,10 +34,12 @@ KERNEL_V3B = 2
 KERNEL_V3_128 = 3  # the fused forward pinned to 128 rows per workgroup
 KERNEL_V3_256 = 4  # pinned to 256 rows per workgroup (one wave group)
 KERNEL_V3_64X4 = 5  # pinned to 64 rows per workgroup split over four KV groups (head_dim 64)
+KERNEL_V3_128X4 = 6  # pinned to 128 rows (two half blocks) walked as one list by four KV groups (head_dim 64)
 KERNEL_IDS = {"v0_unfused": KERNEL_UNFUSED, "v3_mfma": KERNEL_V3, "v3b_mfma": KERNEL_V3B, "v3_128": KERNEL_V3_128,
-              "v3_256": KERNEL_V3_256, "v3_64x4": KERNEL_V3_64X4}
+              "v3_256": KERNEL_V3_256, "v3_64x4": KERNEL_V3_64X4, "v3_128x4": KERNEL_V3_128X4}
 # (rows per workgroup, KV groups) of each pinned fused configuration
-FUSED_CONFIGS = {"v3b_mfma": (64, 2), "v3_128": (128, 2), "v3_256": (256, 1), "v3_64x4": (64, 4)}
+FUSED_CONFIGS = {"v3b_mfma": (64, 2), "v3_128": (128, 2), "v3_256": (256, 1), "v3_64x4": (64, 4),
+                 "v3_128x4": (128, 4)}
 
 _lib = None
 
@@ -317,7 +319,7 @@ def launch_attention_fused(q, k, v, o, shape, causal: bool, rows_per_block: int 
 def launch_attention_fused_groups(q, k, v, o, shape, causal: bool, rows_per_block: int, kv_groups: int,
                                   stream=None) -> bool:
     """The fused forward in a pinned (rows per workgroup, KV groups)
-    configuration: (128, 2), (64, 2), (256, 1) or (64, 4) (head_dim 64)."""
+    configuration: (128, 2), (64, 2), (256, 1), or at head_dim 64 (64, 4) and (128, 4)."""
     s = _shape_of(shape)
     st = lib().fa_launch_attention_fused_groups(_ptr(q), _ptr(k), _ptr(v), _ptr(o), s.batch, s.heads, s.seq_len,
                                                 s.head_dim, int(causal), int(rows_per_block), int(kv_groups),
@@ -399,7 +401,7 @@ def attention_forward(q, k, v, causal: bool = False, kernel: str = "v3_mfma", ou
     elif kernel == "v3b_mfma":
         if not launch_attention_tensorcore_v3b(q, k, v, o, shape, causal):
             raise ValueError(f"head_dim {shape.head_dim} is not supported by the fused kernel")
-    elif kernel in ("v3_128", "v3_256", "v3_64x4"):
+    elif kernel in ("v3_128", "v3_256", "v3_64x4", "v3_128x4"):
         rows, groups = FUSED_CONFIGS[kernel]
         if not launch_attention_fused_groups(q, k, v, o, shape, causal, rows, groups):
             raise ValueError(f"head_dim {shape.head_dim} is not supported by the {kernel} configuration")

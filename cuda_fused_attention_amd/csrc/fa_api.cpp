@@ -187,6 +187,8 @@ int launch_which(int which, const void* q, const void* k, const void* v, void* o
         case 4: return fa_launch_attention_fused(q, k, v, o, batch, heads, seq_len, head_dim, causal, 256, stream);
         case 5:
             return fa_launch_attention_fused_groups(q, k, v, o, batch, heads, seq_len, head_dim, causal, 64, 4, stream);
+        case 6:
+            return fa_launch_attention_fused_groups(q, k, v, o, batch, heads, seq_len, head_dim, causal, 128, 4, stream);
         default: return hipErrorInvalidValue;
     }
 }

@@ -122,25 +122,31 @@ struct TileCopy
 };
 
 // kGroups wave groups of kWpg waves (one wave per 32-row slot in each
-// group): 2 splits the KV range between the groups (split-KV inside the
+// group): 2 or 4 split the KV range between the groups (split-KV inside the
 // workgroup), 1 walks it whole with every wave on one tile stream.
-template <int D, int kWpg, int kGroups = 2>
+// kList: the workgroup holds two half blocks of 32*kWpg rows (2*kWpg slots)
+// and each group walks one quarter of the list "tiles of the first half
+// block, then tiles of the second", on the rows of the half block the tile
+// belongs to (four groups of two waves).
+template <int D, int kWpg, int kGroups = 2, bool kList = false>
 struct Cfg : TileCopy<D, kWpg>
 {
     using TileCopy<D, kWpg>::kIssues;
-    static constexpr int kRows = 32 * kWpg;                            // query rows per workgroup
+    static constexpr int kSlots = kList ? 2 * kWpg : kWpg;            // 32-row Q slots per workgroup
+    static constexpr int kRows = 32 * kSlots;                          // query rows per workgroup
     static constexpr int kThreads = 64 * kGroups * kWpg;
     static constexpr int kTileElems = kTileKV * D;                     // bf16 per K or V tile
     static constexpr int kGroupElems = 2 * kStages * kTileElems;       // one group's K and V stages
     static constexpr int kLdsElems = kGroups * kGroupElems;
-    static constexpr int kQElems = kWpg * 32 * D;                      // Q rows of the kWpg slots
+    static constexpr int kQElems = kSlots * 32 * D;                    // Q rows of the slots
     static constexpr int kQIssues = 32 * D * 2 / 1024;                 // DMA issues per slot's Q rows
     static constexpr int kQRowsPerIssue = 64 / (D / 8);                // rows one (64-lane) Q copy covers
-    static constexpr int kQIssuesPerWave = kQIssues / kGroups;
+    static constexpr int kQIssuesPerWave = kSlots * kQIssues / (kGroups * kWpg);
     static_assert(D == 64 || D == 128, "head_dim 64 or 128");
     static_assert(kGroups == 1 || kGroups == 2 || kGroups == 4, "one, two or four wave groups");
+    static_assert(!kList || (kWpg == 2 && kGroups == 4 && D == 64), "the list layout: four groups of two waves");
     static_assert(2 * kIssues < 64, "vmcnt range");
-    static_assert(kQIssuesPerWave * kGroups == kQIssues, "Q copies split evenly over the waves");
+    static_assert(kQIssuesPerWave * kGroups * kWpg == kSlots * kQIssues, "Q copies split evenly over the waves");
     static_assert((kLdsElems + kQElems) * 2 <= 160 * 1024, "LDS of one workgroup");
 };
 
@@ -470,7 +476,7 @@ __device__ __forceinline__ void rescale_o(Frag<D>& f, float alpha)
         for (int r = 0; r < 16; ++r) f.o[db][r] *= alpha;
 }
 
-template <int D, int kWpg, bool kCausal, int kGroups>
+template <int D, int kWpg, bool kCausal, int kGroups, bool kList = false>
 __global__ __launch_bounds__(64 * kGroups * kWpg) void fused_attention_kernel(const uint16_t* __restrict__ q,
                                                                               const uint16_t* __restrict__ k,
                                                                               const uint16_t* __restrict__ v,
@@ -478,7 +484,7 @@ __global__ __launch_bounds__(64 * kGroups * kWpg) void fused_attention_kernel(co
                                                                               int q_blocks, int total_blocks,
                                                                               float c_log2, int paired)
 {
-    using C = Cfg<D, kWpg, kGroups>;
+    using C = Cfg<D, kWpg, kGroups, kList>;
     // Group g's K stages, then its V stages, at compile-time offsets of one
     // LDS array, so every operand read is a per-lane base plus an immediate;
     // the Q rows of the workgroup's slots follow.
@@ -513,9 +519,19 @@ __global__ __launch_bounds__(64 * kGroups * kWpg) void fused_attention_kernel(co
     //   0..kWpg-1 in order and group 1's are rotated by kWpg/2, so the two
     //   waves sharing a SIMD (w and w + kWpg) hold one early and one late
     //   half block.
+    //   The list layout (kList): the workgroup holds two half blocks A
+    //   (slots 0, 1) and B (slots 2, 3), paired as above for one-round causal
+    //   grids, else the two halves of one block. Its work is the list "K/V
+    //   tiles 0 .. eT-1 on A's rows, then tiles 0 .. lT-1 on B's rows" (eT,
+    //   lT: the tiles each half block needs), split into four contiguous
+    //   quarters, one per group of two waves (wave w holds slot w of the
+    //   half block a tile belongs to). At most one group's quarter crosses
+    //   from A to B: its waves keep A's partial aside and switch to B's rows.
+    //   Every group then computes on every step, so each SIMD keeps two busy
+    //   waves, however unequal the two half blocks' tile counts.
     const int grp_s = __builtin_amdgcn_readfirstlane(grp);
-    const bool pair_rows = kCausal && kGroups == 2 && paired != 0;
-    const int slot = (pair_rows && grp_s == 1) ? (wg_s + kWpg / 2) % kWpg : wg_s;
+    const bool pair_rows = kCausal && (kGroups == 2 || kList) && paired != 0;
+    int slot = (!kList && pair_rows && grp_s == 1) ? (wg_s + kWpg / 2) % kWpg : wg_s;
     constexpr int kHalfRows = C::kRows / 2;
     const int n_half = (n + kHalfRows - 1) / kHalfRows;
     const int pa = qb_in;
@@ -525,12 +541,11 @@ __global__ __launch_bounds__(64 * kGroups * kWpg) void fused_attention_kernel(co
     auto slot_row0 = [&](int s) {
         if (pair_rows)
         {
-            const int half = s < kWpg / 2 ? pa : (pb > pa ? pb : n_half);
-            return half * kHalfRows + 32 * (s % (kWpg / 2));
+            const int half = s < C::kSlots / 2 ? pa : (pb > pa ? pb : n_half);
+            return half * kHalfRows + 32 * (s % (C::kSlots / 2));
         }
         return qb * C::kRows + 32 * s;
     };
-    const int wq0 = slot_row0(slot);
     const int last_row = pair_rows ? (pb > pa ? pb : pa) * kHalfRows + kHalfRows - 1 : qb * C::kRows + C::kRows - 1;
 
     const size_t slab_off = static_cast<size_t>(slab) * n * D;
@@ -541,41 +556,105 @@ __global__ __launch_bounds__(64 * kGroups * kWpg) void fused_attention_kernel(co
 
     const int last_key = kCausal ? min(last_row, n - 1) : n - 1;
     const int n_tiles = last_key / kTileKV + 1;
-    const fa::FusedSplit split = fa::fused_split_n(n_tiles, kGroups);
+    // Tiles of a half block starting at row r0: those its rows may see.
+    auto half_tiles = [&](int r0) {
+        return r0 >= n ? 0 : (kCausal ? min(r0 + kHalfRows - 1, n - 1) : n - 1) / kTileKV + 1;
+    };
+    const int e_tiles = kList ? half_tiles(slot_row0(0)) : 0;  // list items of half block A
+    const int n_items = kList ? e_tiles + half_tiles(slot_row0(C::kSlots / 2)) : n_tiles;
+    const fa::FusedSplit split = fa::fused_split_n(n_items, kGroups);
 
-    // Tiles from t_mask on need the per-element mask (sequence tail, or this
-    // wave's diagonal); tiles after t_last lie wholly above the diagonal.
-    const int t_tail = (n % kTileKV) ? n / kTileKV : n_tiles;
-    const int t_diag = kCausal ? (wq0 + 1) / kTileKV : n_tiles;
-    const int t_mask = min(t_tail, t_diag);
-    // Dense: t_last is n_tiles - 1, passed through readfirstlane so the
-    // compiler cannot fold the per-step tests away; folded, it merges the
-    // step variants and its hoisting then spills at head_dim 128.
-    // Causal waves whose rows all lie past the sequence end compute nothing.
-    const int t_last = kCausal ? (wq0 >= n ? -1 : min((wq0 + 31) / kTileKV, n_tiles - 1))
-                               : __builtin_amdgcn_readfirstlane(n_tiles - 1);
-
-    const int query = wq0 + i;
-    // First key this lane's query may not see, minus 4*h (see mask_tile).
-    const int dead_base = (kCausal ? min(n, query + 1) : n) - 4 * h;
+    // Row-dependent values of the wave's current slot (mutable only in the
+    // list layout, where a wave may move to half block B's rows):
+    //   t_mask: first tile that needs the per-element mask (sequence tail, or
+    //   this wave's diagonal); t_last: last tile not wholly above the
+    //   diagonal (of the tiles up to last_tile). Dense: t_last is
+    //   last_tile, passed through readfirstlane so the compiler cannot fold
+    //   the per-step tests away; folded, it merges the step variants and its
+    //   hoisting then spills at head_dim 128. Causal waves whose rows all lie
+    //   past the sequence end compute nothing. dead_base: first key this
+    //   lane's query may not see, minus 4*h (see mask_tile).
+    int wq0, t_mask, t_last, dead_base;
+    auto set_rows = [&](int s, int last_tile) {
+        wq0 = slot_row0(s);
+        const int t_tail = (n % kTileKV) ? n / kTileKV : last_tile + 1;
+        const int t_diag = kCausal ? (wq0 + 1) / kTileKV : last_tile + 1;
+        t_mask = min(t_tail, t_diag);
+        t_last = kCausal ? (wq0 >= n ? -1 : min((wq0 + 31) / kTileKV, last_tile))
+                         : __builtin_amdgcn_readfirstlane(last_tile);
+        dead_base = (kCausal ? min(n, wq0 + i + 1) : n) - 4 * h;
+    };
+    if constexpr (!kList) set_rows(slot, n_tiles - 1);
 
     Frag<D> f;
     RowState rs;
+    // MFMA B operand ks of slot s's Q rows, from the Q area (laid out like a
+    // K tile), which stays intact until the merge.
+    auto q_ops = [&](int s, int ks) {
+        return *reinterpret_cast<const bf16x8*>(lds + C::kLdsElems + s * 32 * D + i * D +
+                                                (((2 * ks + h) ^ swz_k<D>(i)) << 3));
+    };
+    // The list layout's partial of half block A, kept while a moving wave
+    // computes B's rows.
+    f32x16 o_a[kList ? D / 32 : 1];
+    float m_a = kEmptyBase, l_a = 0.0f;
 
     auto run_group = [&](auto gtag) {
-        constexpr int G = decltype(gtag)::value;
-        uint16_t* const kb = lds + G * C::kGroupElems;            // K stages of this group
+        // The group index: a compile-time constant, or (four groups) a
+        // uniform runtime value, so that all groups run one copy of the
+        // loop (four copies overflow the instruction cache).
+        const int G = gtag;
         // LDS byte addresses of this group's K and V stages (DMA targets):
         // the array's base plus compile-time offsets.
         const uint32_t k_lds = lds_base + G * C::kGroupElems * 2;
         const uint32_t v_lds = k_lds + kStages * C::kTileElems * 2;
-        const int tb = split.first[G];                            // first tile of this group
-        const int cnt = split.count[G];
-        const int lw = min(cnt - 1, t_last - tb);                 // last local tile this wave computes
+        int tb = 0, cnt = 0;  // this group's list items [tb, tb + cnt)
+#pragma unroll
+        for (int g = 0; g < kGroups; ++g)
+            if (g == G)
+            {
+                tb = split.first[g];
+                cnt = split.count[g];
+            }
+        // Local step jj walks list item tb + jj, whose K/V tile is tile0 + jj
+        // (list layout: items from e_tiles on are tiles of half block B).
+        // sw_step: the step after which the waves of a group whose quarter
+        // crosses from A to B move to B's rows (-1: none).
+        const int sw_step = (kList && tb < e_tiles && e_tiles < tb + cnt) ? e_tiles - tb - 1 : -1;
+        int tile0 = tb;
+        const int b_last = n_items - e_tiles - 1;  // list layout: B's last tile
+        // Steps a moving wave computes (A's part, then B's rows up to its
+        // diagonal).
+        int n_moving = 0;
+        if constexpr (kList)
+        {
+            if (tb >= e_tiles)
+            {
+                slot = C::kSlots / 2 + wg_s;
+                set_rows(slot, b_last);
+                tile0 = tb - e_tiles;
+            }
+            else
+            {
+                if (sw_step >= 0)
+                {
+                    set_rows(C::kSlots / 2 + wg_s, b_last);
+                    n_moving = max(sw_step + 1, min(cnt, t_last - (tb - e_tiles) + 1));
+                }
+                set_rows(wg_s, e_tiles - 1);
+            }
+        }
+        // Last local step this wave computes. A wave that moves to B's rows
+        // computes every step of A's part (tiles past its diagonal are
+        // masked whole).
+        int lw = sw_step >= 0 ? sw_step : min(cnt - 1, t_last - tile0);
         // First step whose "next" tile needs the per-element mask: the
         // diagonal / tail tile, or the dummy product after the wave's last
-        // tile (steps run jj <= lw).
-        const int j_mask = min(lw, t_mask - tb - 1);
+        // tile (steps run jj <= lw). From step j_end on nothing is masked:
+        // the next tile of the step before a move is B's first, which the
+        // move itself masks.
+        int j_mask = min(lw, t_mask - tile0 - 1);
+        int j_end = sw_step >= 0 ? sw_step : lw + 1;
 
         // DMA lane offsets (full tiles and the tail tile) and copy helpers.
         // Every copy point issues a fixed number of copies so the vmcnt
@@ -584,7 +663,10 @@ __global__ __launch_bounds__(64 * kGroups * kWpg) void fused_attention_kernel(co
         uint32_t koff[C::kIssues], voff[C::kIssues];
         dma_lane_offsets<D, kWpg, false>(wg, lane, koff);
         dma_lane_offsets<D, kWpg, true>(wg, lane, voff);
-        auto kv_at = [&](int jj) { return min(tb + jj, n_tiles - 1) * kTileKV; };
+        auto kv_at = [&](int jj) {
+            const int it = min(tb + jj, n_items - 1);
+            return (kList && it >= e_tiles ? it - e_tiles : it) * kTileKV;
+        };
         auto copy_k = [&](int jj, int stage, int u) {
             dma_copy<D, kWpg>(tile_rsrc<D>(k_bytes, kv_at(jj), n), k_lds + stage * (C::kTileElems * 2), wg_s, u, lane,
                               koff);
@@ -658,9 +740,7 @@ __global__ __launch_bounds__(64 * kGroups * kWpg) void fused_attention_kernel(co
         wait_vm_lgkm0<(2 * kStages - 2) * C::kIssues>();
         barrier();
 #pragma unroll
-        for (int ks = 0; ks < D / 16; ++ks)
-            f.q[ks] = *reinterpret_cast<const bf16x8*>(lds + C::kLdsElems + slot * 32 * D + i * D +
-                                                       (((2 * ks + h) ^ swz_k<D>(i)) << 3));
+        for (int ks = 0; ks < D / 16; ++ks) f.q[ks] = q_ops(slot, ks);
 
         // Pipeline registers: S^T and the first half of P of the current
         // tile, double-buffered by step parity (no register copies), the
@@ -677,7 +757,7 @@ __global__ __launch_bounds__(64 * kGroups * kWpg) void fused_attention_kernel(co
             load_k_ops<D>(lds, f, ka);
             sbuf[0] = f32x16{};
             qk_part<D, 0, D / 16>(f, ka, sbuf[0]);
-            if (tb >= t_mask) mask_tile(sbuf[0], dead_base - tb * kTileKV);
+            if (tile0 >= t_mask) mask_tile(sbuf[0], dead_base - tile0 * kTileKV);
             // O and l are still zero: the base moves without rescaling.
             rs.m = __builtin_elementwise_maximum(rs.m, row_max_raw(sbuf[0]) * c_log2 + kBaseHeadroom);
             exp_part<0, 0, 8>(sbuf[0], p_lo[0], rs.m, c_log2, tsum);
@@ -719,9 +799,11 @@ __global__ __launch_bounds__(64 * kGroups * kWpg) void fused_attention_kernel(co
         auto rebase = [&](auto par_tag, int jj) {
             constexpr int P = decltype(par_tag)::value;
             constexpr int B = P & 1;
-            const int t = tb + jj;
+            const int t = tile0 + jj;
             const int key = t * kTileKV + i;
             // One K operand at a time (the path is rare; registers are not).
+            // The list layout takes the rows' Q from LDS: on the step before
+            // a move f.q already holds B's rows.
             f32x16 st = {};
 #pragma unroll
             for (int ks = 0; ks < D / 16; ++ks)
@@ -729,7 +811,8 @@ __global__ __launch_bounds__(64 * kGroups * kWpg) void fused_attention_kernel(co
                 const bf16x8 kr = key < n ? *reinterpret_cast<const bf16x8*>(k_slab + static_cast<size_t>(key) * D +
                                                                               (2 * ks + h) * 8)
                                           : bf16x8{};
-                st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kr, f.q[ks], st, 0, 0, 0);
+                const bf16x8 qr = kList ? q_ops(slot, ks) : f.q[ks];
+                st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kr, qr, st, 0, 0, 0);
                 __builtin_amdgcn_sched_barrier(0);
             }
             if (t >= t_mask) mask_tile(st, dead_base - t * kTileKV);
@@ -781,8 +864,8 @@ __global__ __launch_bounds__(64 * kGroups * kWpg) void fused_attention_kernel(co
             // 1 finishes (a per-step trace showed ~350 idle cycles per step
             // at head_dim 64; measured 1% per launch at head_dim 128, 2% at
             // 64).
-            constexpr bool kLeadB = kGroups > 1 && G >= kGroups / 2 && !kCausal;
-            if constexpr (kLeadB) __builtin_amdgcn_s_setprio(1);
+            const bool lead_b = kGroups > 1 && G >= kGroups / 2 && !kCausal;
+            if (lead_b) __builtin_amdgcn_s_setprio(1);
             const bool rare = __any(tsum > kSumLimit);
             if (rare)
             {
@@ -798,8 +881,9 @@ __global__ __launch_bounds__(64 * kGroups * kWpg) void fused_attention_kernel(co
             // exponentials. On the wave's last tile (jj == lw) the "next" S^T
             // is a dummy product with a landed stage: masking all of it makes
             // its P and sums zero.
-            if (jj >= j_mask)
-                mask_tile(sbuf[B ^ 1], jj == lw ? -kTileKV : dead_base - (tb + jj + 1) * kTileKV);
+            const bool mask_next =
+                kList ? static_cast<unsigned>(jj - j_mask) < static_cast<unsigned>(j_end - j_mask) : jj >= j_mask;
+            if (mask_next) mask_tile(sbuf[B ^ 1], jj == lw ? -kTileKV : dead_base - (tile0 + jj + 1) * kTileKV);
             __builtin_amdgcn_sched_barrier(0);
             const bf16x8 p_cur[2] = {p_lo[B], p_hi};
             tsum = 0.0f;
@@ -818,14 +902,51 @@ __global__ __launch_bounds__(64 * kGroups * kWpg) void fused_attention_kernel(co
             pin(tsum);
             if (rare) rebase(par_tag, jj);
             pin(rs.l);
-            if constexpr (kLeadB) __builtin_amdgcn_s_setprio(0);
+            if (lead_b) __builtin_amdgcn_s_setprio(0);
+        };
+
+        // The move to half block B's rows (list layout), after block B of
+        // step sw_step: A's partial is set aside and the walk restarts its
+        // row state on B's first tile, whose S^T block A of this step
+        // already computed with B's Q (loaded before it): mask it, set the
+        // base from its row max, and redo the first half of its
+        // exponentials (block B ran them against A's base).
+        auto move_rows = [&](auto par_tag) {
+            constexpr int B = decltype(par_tag)::value & 1;
+#pragma unroll
+            for (int db = 0; db < D / 32; ++db)
+            {
+                o_a[db] = f.o[db];
+                f.o[db] = f32x16{};
+            }
+            m_a = rs.m;
+            l_a = rs.l;
+            slot = C::kSlots / 2 + wg_s;
+            set_rows(slot, b_last);
+            tile0 = tb - e_tiles;
+            lw = min(cnt - 1, t_last - tile0);
+            j_mask = min(lw, t_mask - tile0 - 1);
+            j_end = lw + 1;
+            if (t_mask <= 0) mask_tile(sbuf[B ^ 1], dead_base);
+            rs.m = __builtin_elementwise_maximum(kEmptyBase, row_max_raw(sbuf[B ^ 1]) * c_log2 + kBaseHeadroom);
+            rs.l = 0.0f;
+            tsum = 0.0f;
+            exp_part<0, 0, 8>(sbuf[B ^ 1], p_lo[B ^ 1], rs.m, c_log2, tsum);
         };
 
         // Steps this wave computes (tiles up to its diagonal / the group's
         // end), then the group's remaining steps, in which the wave only
         // issues its share of the copies and joins the barriers. Two loops,
         // so the computing loop carries no idle branch.
-        const int n_active = min(cnt, lw + 1);
+        const int n_active = sw_step >= 0 ? n_moving : min(cnt, lw + 1);
+        // Block A of step sw_step computes B's first S^T: B's Q is loaded at
+        // the end of the step before (here, when that is the prologue).
+        auto load_b_q = [&]() {
+#pragma unroll
+            for (int ks = 0; ks < D / 16; ++ks) f.q[ks] = q_ops(C::kSlots / 2 + wg_s, ks);
+        };
+        if constexpr (kList)
+            if (sw_step == 0) load_b_q();
         fa::fused_group_walk(n_active, [&](auto par_tag, int jj) {
             block_a(par_tag, jj);
             // Only the copies of steps jj-1 and jj may still be in flight:
@@ -836,6 +957,16 @@ __global__ __launch_bounds__(64 * kGroups * kWpg) void fused_attention_kernel(co
             wait_vm_lgkm0<3 * C::kIssues>();
             barrier();
             block_b(par_tag, jj);
+            if constexpr (kList)
+            {
+                // One test per step for both events (steps sw_step - 1 and
+                // sw_step; never when sw_step is -1).
+                if (static_cast<unsigned>(jj - sw_step + 1) <= 1u)
+                {
+                    if (jj == sw_step) move_rows(par_tag);
+                    else load_b_q();
+                }
+            }
         });
         for (int jj = max(n_active, 0); jj < cnt; ++jj)
         {
@@ -862,11 +993,7 @@ __global__ __launch_bounds__(64 * kGroups * kWpg) void fused_attention_kernel(co
     }
     else
     {
-        const int g4 = __builtin_amdgcn_readfirstlane(grp);
-        if (g4 == 0) run_group(std::integral_constant<int, 0>{});
-        else if (g4 == 1) run_group(std::integral_constant<int, 1>{});
-        else if (g4 == 2) run_group(std::integral_constant<int, 2>{});
-        else run_group(std::integral_constant<int, 3>{});
+        run_group(grp_s);
     }
 
     // Normalise O^T blocks [kFirstDb, kFirstDb + kNumDb) of this wave's 32
@@ -874,7 +1001,7 @@ __global__ __launch_bounds__(64 * kGroups * kWpg) void fused_attention_kernel(co
     // query) is transposed through `obuf` (32 rows of 32*kNumDb bf16, only
     // this wave touches it now) into row-major bf16 with XOR-swizzled 16-byte
     // chunks, then stored as contiguous 16-byte pieces of the rows.
-    auto store_rows = [&](auto first_tag, auto num_tag, uint16_t* obuf, float inv) {
+    auto store_rows = [&](auto first_tag, auto num_tag, uint16_t* obuf, float inv, int row0) {
         constexpr int kFirstDb = decltype(first_tag)::value;
         constexpr int kNumDb = decltype(num_tag)::value;
         constexpr int kCols = 32 * kNumDb;
@@ -898,8 +1025,8 @@ __global__ __launch_bounds__(64 * kGroups * kWpg) void fused_attention_kernel(co
             const int row = x / kColChunks;
             const int c = x % kColChunks;
             const uint4 chunk = *reinterpret_cast<const uint4*>(obuf + row * kCols + ((c ^ (row & (kColChunks - 1))) * 8));
-            if (wq0 + row < n)
-                *reinterpret_cast<uint4*>(o + slab_off + static_cast<size_t>(wq0 + row) * D + kFirstDb * 32 + c * 8) = chunk;
+            if (row0 + row < n)
+                *reinterpret_cast<uint4*>(o + slab_off + static_cast<size_t>(row0 + row) * D + kFirstDb * 32 + c * 8) = chunk;
         }
     };
 
@@ -914,7 +1041,153 @@ __global__ __launch_bounds__(64 * kGroups * kWpg) void fused_attention_kernel(co
         return l_tot > 0.0f ? __builtin_amdgcn_rcpf(l_tot) : 0.0f;
     };
 
-    if constexpr (kGroups == 1)
+    if constexpr (kList)
+    {
+        // List layout. The holders of half block X are the groups whose
+        // quarter covers some of X's tiles (a contiguous range of groups);
+        // group g holds A's partial (f.o, or o_a if it moved) and / or B's
+        // (f.o). Each half of the head dims of X's rows is finalised by one
+        // holder, which folds the other holders' partials of that half into
+        // its own: a lone holder finalises both halves from its registers;
+        // otherwise groups 0 and 1 finalise A (the first two holders) and
+        // the last two holders B. Every holder writes to an LDS record only
+        // the halves other waves finalise (the least LDS traffic), then one
+        // barrier, then the finalisers fold, normalise and store.
+        constexpr int kFull = (D / 32) * 16 * 64;  // one wave's O^T
+        constexpr int kRec = kFull + 128;
+        constexpr int kRecords = 2 * (kGroups + 1);
+        constexpr int kObuf = 32 * D;              // bf16 of one wave's 32-row store staging
+        static_assert(D == 64, "two 32-dim halves");
+        static_assert(kRecords * kRec * 4 + kGroups * kWpg * kObuf * 2 <= (C::kLdsElems + C::kQElems) * 2,
+                      "records and store staging fit the LDS array");
+        float* const recs = reinterpret_cast<float*>(lds);
+        // Holders: A = [0, a_hi], B = [b_lo, b_hi]; g_cross holds both.
+        int g_cross = kGroups, a_hi = -1, b_lo = kGroups, b_hi = -1;
+#pragma unroll
+        for (int g = 0; g < kGroups; ++g)
+        {
+            const int g0 = split.first[g];
+            const int gc = split.count[g];
+            if (gc > 0 && g0 < e_tiles) a_hi = g;
+            if (gc > 0 && g0 + gc > e_tiles)
+            {
+                b_lo = min(b_lo, g);
+                b_hi = g;
+            }
+            if (g0 < e_tiles && e_tiles < g0 + gc) g_cross = g;
+        }
+        // The record of holder g's partial of half block `half`.
+        auto record = [&](int g, int half, int w) {
+            const int part = (half == 1 && g == g_cross) ? 1 : 0;
+            return recs + ((g + part + (g_cross < g ? 1 : 0)) * kWpg + w) * kRec;
+        };
+        // Finaliser of head-dim half dh of half block `half` (a lone holder
+        // takes both halves).
+        auto finaliser = [&](int half, int dh) {
+            if (half == 0) return a_hi == 0 ? 0 : dh;
+            return b_hi == b_lo ? b_hi : b_hi - 1 + dh;
+        };
+        auto put_half = [&](float* r, const f32x16 (&oo)[D / 32], int dh) {
+#pragma unroll
+            for (int r4 = 0; r4 < 4; ++r4)
+            {
+                const f32x4 v4 = {oo[dh][4 * r4], oo[dh][4 * r4 + 1], oo[dh][4 * r4 + 2], oo[dh][4 * r4 + 3]};
+                *reinterpret_cast<f32x4*>(r + ((dh * 4 + r4) * 64 + lane) * 4) = v4;
+            }
+        };
+        // Write what other waves finalise of this wave's partial of `half`.
+        auto publish = [&](int half, const f32x16 (&oo)[D / 32], float m, float l) {
+            float* const r = record(grp_s, half, wg_s);
+            const bool w0 = finaliser(half, 0) != grp_s;
+            const bool w1 = finaliser(half, 1) != grp_s;
+            if (w0) put_half(r, oo, 0);
+            if (w1) put_half(r, oo, 1);
+            if (w0 || w1)
+            {
+                r[kFull + lane] = m;
+                r[kFull + 64 + lane] = l;
+            }
+        };
+        const bool has_a = grp_s <= a_hi;
+        const bool has_b = grp_s >= b_lo && grp_s <= b_hi;
+        if (has_a)
+        {
+            if (grp_s == g_cross) publish(0, o_a, m_a, l_a);
+            else publish(0, f.o, rs.m, rs.l);
+        }
+        if (has_b) publish(1, f.o, rs.m, rs.l);
+        wait_vm_lgkm0<0>();
+        barrier();
+
+        uint16_t* const obuf = reinterpret_cast<uint16_t*>(recs + kRecords * kRec) + (grp_s * kWpg + wg_s) * kObuf;
+        // A lone holder stores both halves of its rows from its registers.
+        auto store_alone = [&](int half, const f32x16 (&oo)[D / 32], float l) {
+#pragma unroll
+            for (int b = 0; b < D / 32; ++b) f.o[b] = oo[b];
+            store_rows(std::integral_constant<int, 0>{}, std::integral_constant<int, D / 32>{}, obuf, inv_row_sum(l),
+                       slot_row0(half * kWpg + wg_s));
+        };
+        // Finalise head-dim half DH of half block `half` from this wave's
+        // partial (oo, m, l) and the records of the other holders [lo, hi]:
+        // every record's values are loaded first, then folded against the
+        // common maximum (one LDS round trip, independent exponentials).
+        auto finalise = [&](auto dh_tag, int half, const f32x16 (&oo)[D / 32], float m, float l, int lo, int hi) {
+            constexpr int DH = decltype(dh_tag)::value;
+            float mr[kGroups], lr[kGroups];
+            f32x4 xr[kGroups][4];
+#pragma unroll
+            for (int g = 0; g < kGroups; ++g)
+            {
+                mr[g] = kEmptyBase;
+                lr[g] = 0.0f;
+                if (g >= lo && g <= hi && g != grp_s)
+                {
+                    const float* r = record(g, half, wg_s);
+                    mr[g] = r[kFull + lane];
+                    lr[g] = r[kFull + 64 + lane];
+#pragma unroll
+                    for (int r4 = 0; r4 < 4; ++r4)
+                        xr[g][r4] = *reinterpret_cast<const f32x4*>(r + ((DH * 4 + r4) * 64 + lane) * 4);
+                }
+            }
+            float m_new = m;
+#pragma unroll
+            for (int g = 0; g < kGroups; ++g) m_new = __builtin_elementwise_maximum(m_new, mr[g]);
+            const float a0 = __builtin_amdgcn_exp2f(m - m_new);
+            float acc_l = l * a0;
+            f32x16 acc;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[e] = oo[DH][e] * a0;
+#pragma unroll
+            for (int g = 0; g < kGroups; ++g)
+            {
+                if (g >= lo && g <= hi && g != grp_s)
+                {
+                    const float a = __builtin_amdgcn_exp2f(mr[g] - m_new);
+                    acc_l += lr[g] * a;
+#pragma unroll
+                    for (int r4 = 0; r4 < 4; ++r4)
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) acc[4 * r4 + j] += xr[g][r4][j] * a;
+                }
+            }
+            f.o[DH] = acc;
+            store_rows(std::integral_constant<int, DH>{}, std::integral_constant<int, 1>{}, obuf, inv_row_sum(acc_l),
+                       slot_row0(half * kWpg + wg_s));
+        };
+        auto finish_half = [&](int half, const f32x16 (&oo)[D / 32], float m, float l, int lo, int hi) {
+            if (lo == hi) store_alone(half, oo, l);
+            else if (finaliser(half, 0) == grp_s) finalise(std::integral_constant<int, 0>{}, half, oo, m, l, lo, hi);
+            else finalise(std::integral_constant<int, 1>{}, half, oo, m, l, lo, hi);
+        };
+        if (has_a && (finaliser(0, 0) == grp_s || finaliser(0, 1) == grp_s))
+        {
+            if (grp_s == g_cross) finish_half(0, o_a, m_a, l_a, 0, a_hi);
+            else finish_half(0, f.o, rs.m, rs.l, 0, a_hi);
+        }
+        if (has_b && (finaliser(1, 0) == grp_s || finaliser(1, 1) == grp_s)) finish_half(1, f.o, rs.m, rs.l, b_lo, b_hi);
+    }
+    else if constexpr (kGroups == 1)
     {
         // One group: every wave holds its rows' whole O^T. All DMAs have
         // landed (every wave drained its own before the last barrier), so
@@ -922,7 +1195,7 @@ __global__ __launch_bounds__(64 * kGroups * kWpg) void fused_attention_kernel(co
         // rows of it.
         static_assert(kWpg * 32 * D <= C::kLdsElems, "transpose staging fits the stage area");
         store_rows(std::integral_constant<int, 0>{}, std::integral_constant<int, D / 32>{}, lds + slot * 32 * D,
-                   inv_row_sum(rs.l));
+                   inv_row_sum(rs.l), wq0);
     }
     else
     {
@@ -977,7 +1250,7 @@ __global__ __launch_bounds__(64 * kGroups * kWpg) void fused_attention_kernel(co
         const float inv = inv_row_sum(l);
         wait_vm_lgkm0<0>();  // received values are in registers before the area is reused
         store_rows(std::integral_constant<int, kKeep>{}, std::integral_constant<int, kHalfDb>{},
-                   reinterpret_cast<uint16_t*>(x_recv), inv);
+                   reinterpret_cast<uint16_t*>(x_recv), inv, wq0);
     };
     if constexpr (kGroups == 4)
     {
@@ -1033,37 +1306,38 @@ __global__ __launch_bounds__(64 * kGroups * kWpg) void fused_attention_kernel(co
     }
 }
 
-template <int D, int kWpg, bool kCausal, int kGroups>
+template <int D, int kWpg, bool kCausal, int kGroups, bool kList = false>
 const void* kernel_ptr()
 {
-    return reinterpret_cast<const void*>(&fused_attention_kernel<D, kWpg, kCausal, kGroups>);
+    return reinterpret_cast<const void*>(&fused_attention_kernel<D, kWpg, kCausal, kGroups, kList>);
 }
 
 // Whether a workgroup configuration exists for head_dim D: four KV groups
 // need four stage sets, which fit a CU's 160 KiB of LDS at head_dim 64 only.
-template <int kWpg, int kGroups>
+template <int kWpg, int kGroups, bool kList = false>
 constexpr bool has_config(int head_dim)
 {
     return head_dim == 64 || (head_dim == 128 && kGroups != 4);
 }
 
-template <int kWpg, int kGroups>
+template <int kWpg, int kGroups, bool kList = false>
 const void* pick_kernel(int head_dim, bool causal)
 {
-    if (head_dim == 64) return causal ? kernel_ptr<64, kWpg, true, kGroups>() : kernel_ptr<64, kWpg, false, kGroups>();
-    if constexpr (has_config<kWpg, kGroups>(128))
+    if (head_dim == 64)
+        return causal ? kernel_ptr<64, kWpg, true, kGroups, kList>() : kernel_ptr<64, kWpg, false, kGroups, kList>();
+    if constexpr (has_config<kWpg, kGroups, kList>(128))
         if (head_dim == 128)
             return causal ? kernel_ptr<128, kWpg, true, kGroups>() : kernel_ptr<128, kWpg, false, kGroups>();
     return nullptr;
 }
 
-template <int D, int kWpg, bool kCausal, int kGroups>
+template <int D, int kWpg, bool kCausal, int kGroups, bool kList = false>
 hipError_t launch_typed(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o, int n, int q_blocks,
                         int total, float c_log2, int paired, hipStream_t stream)
 {
-    return fa::launch_kernel(fused_attention_kernel<D, kWpg, kCausal, kGroups>, dim3(static_cast<unsigned>(total)),
-                             dim3(Cfg<D, kWpg, kGroups>::kThreads), stream, q, k, v, o, n, q_blocks, total, c_log2,
-                             paired);
+    return fa::launch_kernel(fused_attention_kernel<D, kWpg, kCausal, kGroups, kList>,
+                             dim3(static_cast<unsigned>(total)), dim3(Cfg<D, kWpg, kGroups, kList>::kThreads), stream,
+                             q, k, v, o, n, q_blocks, total, c_log2, paired);
 }
 
 // Compute units of the current device (cached per device; 256 on an
@@ -1083,11 +1357,11 @@ int device_compute_units()
     return cus;
 }
 
-template <int kWpg, int kGroups = 2>
+template <int kWpg, int kGroups = 2, bool kList = false>
 int launch_fused(const void* q, const void* k, const void* v, void* o, int batch, int heads, int seq_len,
                  int head_dim, int causal, void* stream_ptr)
 {
-    if (!has_config<kWpg, kGroups>(head_dim)) return FA_ERROR_UNSUPPORTED;
+    if (!has_config<kWpg, kGroups, kList>(head_dim)) return FA_ERROR_UNSUPPORTED;
     if (batch < 0 || heads < 0 || seq_len < 0) return hipErrorInvalidValue;
     const long long bh = static_cast<long long>(batch) * heads;
     if (bh == 0 || seq_len == 0) return hipSuccess;
@@ -1103,10 +1377,10 @@ int launch_fused(const void* q, const void* k, const void* v, void* o, int batch
     // blocks (p, last - p), which evens out the triangle's work per
     // workgroup (two-group configurations). Larger causal grids keep whole
     // blocks, issued heaviest first, and the dispatcher balances the rounds.
-    constexpr int rows = 32 * kWpg;
+    constexpr int rows = 32 * kWpg * (kList ? 2 : 1);
     constexpr int threads = 64 * kGroups * kWpg;
     const long long blocks = (static_cast<long long>(seq_len) + rows - 1) / rows;
-    const int paired = (kGroups == 2 && causal && bh * blocks <= device_compute_units()) ? 1 : 0;
+    const int paired = ((kGroups == 2 || kList) && causal && bh * blocks <= device_compute_units()) ? 1 : 0;
     const long long q_blocks = paired ? ((static_cast<long long>(seq_len) + rows / 2 - 1) / (rows / 2) + 1) / 2 : blocks;
     const long long total = bh * q_blocks;
     if (total > 0x7fffffffLL / threads) return hipErrorInvalidValue;
@@ -1120,9 +1394,11 @@ int launch_fused(const void* q, const void* k, const void* v, void* o, int batch
     const int qbk = static_cast<int>(q_blocks);
     const int tot = static_cast<int>(total);
     if (head_dim == 64)
-        return causal ? launch_typed<64, kWpg, true, kGroups>(qb, kb, vb, ob, seq_len, qbk, tot, c_log2, paired, stream)
-                      : launch_typed<64, kWpg, false, kGroups>(qb, kb, vb, ob, seq_len, qbk, tot, c_log2, 0, stream);
-    if constexpr (has_config<kWpg, kGroups>(128))
+        return causal ? launch_typed<64, kWpg, true, kGroups, kList>(qb, kb, vb, ob, seq_len, qbk, tot, c_log2, paired,
+                                                                     stream)
+                      : launch_typed<64, kWpg, false, kGroups, kList>(qb, kb, vb, ob, seq_len, qbk, tot, c_log2, 0,
+                                                                      stream);
+    if constexpr (has_config<kWpg, kGroups, kList>(128))
         return causal ? launch_typed<128, kWpg, true, kGroups>(qb, kb, vb, ob, seq_len, qbk, tot, c_log2, paired, stream)
                       : launch_typed<128, kWpg, false, kGroups>(qb, kb, vb, ob, seq_len, qbk, tot, c_log2, 0, stream);
     return FA_ERROR_UNSUPPORTED;
@@ -1140,6 +1416,13 @@ int launch_fused(const void* q, const void* k, const void* v, void* o, int batch
 //     rounds of them: half the L2->LDS copies per score and no merge, 2-7%
 //     faster there; shorter causal sequences lose more to the coarser
 //     diagonal blocks than they gain;
+//   * head_dim 64, causal, exactly one round of 128-row workgroups and
+//     seq_len >= 2048: the list layout (128 rows, four groups of two waves
+//     walking the two half blocks' tiles as one list), which keeps two busy
+//     waves on every SIMD where the paired two-group layout has one for most
+//     steps ((1,4,8192,64) 46.5 -> 42.3 us, (1,8,4096,64) 26.4 -> 24.3 us,
+//     (2,8,2048,64) 15.7 -> 15.5 us; at seq_len 1024 its merge and deeper
+//     prologue cost more than it saves);
 //   * head_dim 64, causal, more than one round of 128-row workgroups and
 //     seq_len <= 2048: 64 rows in two groups, two workgroups resident per CU
 //     (80 KiB of LDS each), whose prologues and epilogues overlap the other's
@@ -1167,23 +1450,24 @@ FusedConfig auto_config(int batch, int heads, int seq_len, int head_dim, int cau
         if (causal ? (seq_len >= 8192 && wide >= 2 * cus) : wide >= cus) return {256, 1};
         return {128, 2};
     }
+    if (causal && blocks128 == cus && seq_len >= 2048) return {128, 4};
     if (causal && blocks128 > cus && seq_len <= 2048) return {64, 2};
     return {128, 2};
 }
 
-template <int kWpg, int kGroups = 2>
+template <int kWpg, int kGroups = 2, bool kList = false>
 int query_fused(int head_dim, fa_tiling_info* info)
 {
     if (!info) return hipErrorInvalidValue;
     *info = fa_tiling_info{};
-    const void* func = pick_kernel<kWpg, kGroups>(head_dim, false);
+    const void* func = pick_kernel<kWpg, kGroups, kList>(head_dim, false);
     if (!func) return hipSuccess;  // supported = 0
     info->supported = 1;
     info->block_size = 64 * kGroups * kWpg;
     info->waves_per_block = kGroups * kWpg;
     info->kv_groups = kGroups;
     info->tile_kv = kTileKV;
-    info->rows_per_block = 32 * kWpg;
+    info->rows_per_block = 32 * kWpg * (kList ? 2 : 1);
 
     hipFuncAttributes attr{};
     hipError_t e = hipFuncGetAttributes(&attr, func);
@@ -1216,7 +1500,8 @@ int query_fused(int head_dim, fa_tiling_info* info)
     for (int x = 0; x < fa::kFusedKernelResourceCount; ++x)
     {
         const fa::KernelResources& r = fa::kFusedKernelResources[x];
-        if (r.head_dim == head_dim && r.waves_per_group == kWpg && r.groups == kGroups && r.causal == 0)
+        if (r.head_dim == head_dim && r.waves_per_group == kWpg && r.groups == kGroups && r.list == (kList ? 1 : 0) &&
+            r.causal == 0)
             info->agprs_per_thread = r.agprs;
     }
     return hipSuccess;
@@ -1279,6 +1564,8 @@ int fa_launch_attention_fused_groups(const void* q, const void* k, const void* v
         status = launch_fused<8, 1>(q, k, v, o, batch, heads, seq_len, head_dim, causal, stream);
     else if (rows_per_block == 64 && kv_groups == 4)
         status = launch_fused<2, 4>(q, k, v, o, batch, heads, seq_len, head_dim, causal, stream);
+    else if (rows_per_block == 128 && kv_groups == 4)
+        status = launch_fused<2, 4, true>(q, k, v, o, batch, heads, seq_len, head_dim, causal, stream);
     return fa::record_status(status);
 }
 
@@ -1311,6 +1598,7 @@ int fa_query_fused_groups(int head_dim, int rows_per_block, int kv_groups, fa_ti
     else if (rows_per_block == 64 && kv_groups == 2) status = query_fused<2>(head_dim, info);
     else if (rows_per_block == 256 && kv_groups == 1) status = query_fused<8, 1>(head_dim, info);
     else if (rows_per_block == 64 && kv_groups == 4) status = query_fused<2, 4>(head_dim, info);
+    else if (rows_per_block == 128 && kv_groups == 4) status = query_fused<2, 4, true>(head_dim, info);
     return fa::record_status(status);
 }
 

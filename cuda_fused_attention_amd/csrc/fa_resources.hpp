@@ -13,6 +13,7 @@ struct KernelResources
     int waves_per_group;  // kWpg
     int causal;           // kCausal
     int groups;           // kGroups
+    int list;             // kList (two half blocks walked as one list)
     int vgprs;            // architectural VGPRs
     int agprs;            // accumulation VGPRs
     int sgprs;            // scalar registers (total)

@@ -151,9 +151,14 @@ int fa_launch_attention_fused(const void* q, const void* k, const void* v, void*
 /* No counterpart in the reference: the fused forward in any of its workgroup
  * configurations, named by query rows per workgroup and the number of wave
  * groups that split the KV range: (128, 2) is v3's default, (64, 2) v3b,
- * (256, 1) one group of 8 waves, (64, 4) four groups of 2 waves (head_dim 64
+ * (256, 1) one group of 8 waves, (64, 4) four groups of 2 waves, and
+ * (128, 4): two 64-row half blocks whose K/V tiles form one list (the first
+ * half block's tiles, then the second's), walked in four quarters by four
+ * groups of 2 waves that move to the second half block's rows where their
+ * quarter crosses into it; every group works on every step however unequal
+ * the half blocks' causal tile counts. The last two exist at head_dim 64
  * only: FA_ERROR_UNSUPPORTED at 128, whose four stage sets would not fit
- * LDS). Other pairs return hipErrorInvalidValue. */
+ * LDS. Other pairs return hipErrorInvalidValue. */
 int fa_launch_attention_fused_groups(const void* q, const void* k, const void* v, void* o,
                                      int batch, int heads, int seq_len, int head_dim,
                                      int causal, int rows_per_block, int kv_groups, void* stream);

@@ -52,8 +52,9 @@ def run(fa, kernel: str, q, k, v, causal: bool, stream=None, out=None):
         assert fa.launch_attention_fused(q, k, v, o, shape, causal, rows_per_block=128, stream=st)
     elif kernel == "v3_256":
         assert fa.launch_attention_fused(q, k, v, o, shape, causal, rows_per_block=256, stream=st)
-    elif kernel == "v3_64x4":
-        assert fa.launch_attention_fused_groups(q, k, v, o, shape, causal, 64, 4, stream=st)
+    elif kernel in ("v3_64x4", "v3_128x4"):
+        rows, groups = fa.FUSED_CONFIGS[kernel]
+        assert fa.launch_attention_fused_groups(q, k, v, o, shape, causal, rows, groups, stream=st)
     else:
         raise ValueError(kernel)
     torch.cuda.synchronize()
@@ -66,17 +67,18 @@ def run_bits(fa, kernel, qb, kb, vb, causal):
 
 
 # v3_mfma picks its workgroup configuration from the shape (64 rows for
-# grids that leave CUs idle); v3_128, v3_256 and v3_64x4 pin the 128-row,
-# the one-group 256-row and the four-group 64-row ones, so every shape
-# exercises each (v3_64x4 exists for head_dim 64 only).
-KERNELS = ["v0_unfused", "v3_mfma", "v3b_mfma", "v3_128", "v3_256", "v3_64x4"]
-FUSED_KERNELS = ["v3_mfma", "v3b_mfma", "v3_128", "v3_256", "v3_64x4"]
+# grids that leave CUs idle); v3_128, v3_256, v3_64x4 and v3_128x4 pin the
+# 128-row, the one-group 256-row, the four-group 64-row and the four-group
+# 128-row list configurations, so every shape exercises each (the last two
+# exist for head_dim 64 only).
+KERNELS = ["v0_unfused", "v3_mfma", "v3b_mfma", "v3_128", "v3_256", "v3_64x4", "v3_128x4"]
+FUSED_KERNELS = ["v3_mfma", "v3b_mfma", "v3_128", "v3_256", "v3_64x4", "v3_128x4"]
 
 
 def supports(kernel: str, head_dim: int) -> bool:
-    """Whether `kernel` handles head_dim (the four-group configuration's
+    """Whether `kernel` handles head_dim (the four-group configurations'
     stage sets fit LDS at head_dim 64 only)."""
-    return not (kernel == "v3_64x4" and head_dim != 64)
+    return not (kernel in ("v3_64x4", "v3_128x4") and head_dim != 64)
 
 
 def kernels_for(head_dim: int, kernels=None):

@@ -407,7 +407,7 @@ int main(int argc, char** argv)
     // AGPRs of the compiler's resource report.
     std::printf("\nMFMA kernel configurations (fa_query_fused_groups):\n  %8s %9s %8s %6s %6s %6s %6s %12s %10s\n",
                 "q_rows", "kv_groups", "head_dim", "waves", "block", "VGPRs", "AGPRs", "shared/block", "blocks/CU");
-    for (const auto& [rows, groups] : {std::pair{64, 2}, std::pair{64, 4}, std::pair{128, 2}, std::pair{256, 1}})
+    for (const auto& [rows, groups] : {std::pair{64, 2}, std::pair{64, 4}, std::pair{128, 2}, std::pair{128, 4}, std::pair{256, 1}})
         for (int d : {64, 128})
         {
             fa_tiling_info info{};

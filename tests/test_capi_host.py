@@ -56,7 +56,7 @@ def test_host_models_match_oracle(fa_lib, oracle_mod):
             # the model follows the configuration the v3 entry runs at this shape
             rows = fa_lib.tensorcore_v3_rows_per_block(shape, causal)
             assert rows in (64, 128, 256)
-            assert fa_lib.tensorcore_v3_config(shape, causal) in ((64, 2), (64, 4), (128, 2), (256, 1))
+            assert fa_lib.tensorcore_v3_config(shape, causal) in ((64, 2), (64, 4), (128, 2), (128, 4), (256, 1))
             assert fa_lib.tensorcore_v3_config(shape, causal)[0] == rows
             assert fa_lib.tensorcore_v3_hbm_bytes(shape, causal) == L.fa_oracle_blocked_kv_hbm_bytes(B, H, N, D, int(causal), rows, 32)
             assert fa_lib.tensorcore_v3b_hbm_bytes(shape, causal) == L.fa_oracle_blocked_kv_hbm_bytes(B, H, N, D, int(causal), 64, 32)
@@ -88,12 +88,16 @@ def test_error_state_records_host_side_rejections(fa_lib):
 
 def test_configuration_rule_without_a_device(fa_lib):
     """The v3 configuration rule on the CPU (the CU count falls back to an
-    MI355X's 256): the four (2,8,2048,D) metric shapes run 128 rows in two
-    groups; small head_dim-64 grids take four KV groups; an unsupported
-    head_dim reports no configuration."""
+    MI355X's 256): three of the four (2,8,2048,D) metric shapes run 128 rows
+    in two groups and (2,8,2048,64) causal, one round of 128-row workgroups,
+    the four-group list layout; small head_dim-64 grids take four KV groups;
+    an unsupported head_dim reports no configuration."""
     for d in (64, 128):
         for causal in (False, True):
-            assert fa_lib.tensorcore_v3_config((2, 8, 2048, d), causal) == (128, 2)
+            want = (128, 4) if (d, causal) == (64, True) else (128, 2)
+            assert fa_lib.tensorcore_v3_config((2, 8, 2048, d), causal) == want
+    assert fa_lib.tensorcore_v3_config((4, 8, 1024, 64), True) == (128, 2)
+    assert fa_lib.tensorcore_v3_config((1, 4, 8192, 64), True) == (128, 4)
     assert fa_lib.tensorcore_v3_config((1, 8, 2048, 64), True) == (64, 4)
     assert fa_lib.tensorcore_v3_config((1, 8, 512, 64), False) == (64, 2)
     assert fa_lib.tensorcore_v3_config((4, 8, 8192, 64), False) == (128, 2)

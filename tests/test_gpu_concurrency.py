@@ -19,7 +19,7 @@ def test_two_threads_two_streams(fa, oracle_mod):
 
     cases = [((2, 4, 777, 64), True, "v3_mfma"), ((1, 3, 1024, 128), False, "v3_mfma"),
              ((1, 2, 300, 64), True, "v0_unfused"), ((2, 2, 513, 128), True, "v3_256"),
-             ((1, 4, 900, 64), False, "v3_64x4")]
+             ((1, 4, 900, 64), False, "v3_64x4"), ((2, 3, 1000, 64), True, "v3_128x4")]
     inputs, alone = [], []
     for i, (shape, causal, kernel) in enumerate(cases):
         q, k, v = (to_dev(x) for x in oracle_mod.make_inputs(*shape, seeds={"q": 70 + i, "k": 80 + i, "v": 90 + i}))

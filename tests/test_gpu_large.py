@@ -31,7 +31,7 @@ def test_tensors_past_4_gib(fa, oracle_mod):
     host = {s: tuple(from_dev(t[0, s]).reshape(1, 1, N, D) for t in (q, k, v)) for s in slabs}
     for causal in (False, True):
         refs = {s: oracle_mod.attention(*host[s], causal).reshape(N, D) for s in slabs}
-        for kernel in ("v3_mfma", "v3_128", "v3_64x4"):
+        for kernel in ("v3_mfma", "v3_128", "v3_64x4", "v3_128x4"):
             say("large", kernel, causal)
             o = run(fa, kernel, q, k, v, causal, out=nan_like(q))
             for s in slabs:

@@ -197,8 +197,9 @@ def test_v3_picks_the_configuration_by_grid(fa, oracle_mod):
     at head_dim 64 with seq_len >= 1024, else two); at head_dim 128, 256 rows
     in one group when even 256-row workgroups give every CU one (dense) or,
     causal, for seq_len >= 8192 with two rounds of them; at head_dim 64,
-    causal, more than one round and seq_len <= 2048, 64 rows in two groups;
-    else 128 rows in two groups. Its output equals the pinned configuration's
+    causal, exactly one round and seq_len >= 2048, the four-group list layout
+    (128, 4); at head_dim 64, causal, more than one round and seq_len <= 2048,
+    64 rows in two groups; else 128 rows in two groups. Its output equals the pinned configuration's
     bit for bit on each side of each threshold."""
     cus = fa.query_tensorcore_v3(64)["compute_units"]
     assert cus > 0
@@ -210,6 +211,8 @@ def test_v3_picks_the_configuration_by_grid(fa, oracle_mod):
         ((1, cus // 2, 256, 128), (False, True), "v3_128"),     # `cus` of 128 rows, `cus`/2 of 256
         ((1, cus, 256, 128), (False,), "v3_256"),               # `cus` workgroups of 256 rows, dense
         ((1, cus, 256, 64), (False,), "v3_128"),                # head_dim 64: never 256 rows
+        ((1, cus // 16, 2048, 64), (True,), "v3_128x4"),        # head_dim 64 causal, one round, seq_len 2048
+        ((1, cus // 16, 2048, 64), (False,), "v3_128"),         # ... dense
         ((1, cus // 8, 2048, 64), (True,), "v3b_mfma"),         # head_dim 64 causal, 2 rounds, seq_len 2048
         ((1, cus // 16, 4096, 64), (True,), "v3_128"),          # ... and seq_len 4096
         ((1, 2 * cus // 32, 8192, 128), (True,), "v3_256"),     # causal, 2 * `cus` of 256 rows
@@ -336,6 +339,15 @@ def test_error_paths_leave_output_untouched(fa, oracle_mod):
 
 
 def test_query_reports_resources(fa):
+    for rows, groups in fa.FUSED_CONFIGS.values():
+        for d in (64, 128):
+            info = fa.query_fused_groups(d, rows, groups)
+            if groups == 4 and d == 128:
+                assert info["supported"] == 0
+                continue
+            assert info["supported"] == 1 and info["rows_per_block"] == rows and info["kv_groups"] == groups
+            assert info["waves_per_block"] * 64 == info["block_size"] and info["local_bytes_per_thread"] == 0
+            assert info["agprs_per_thread"] == 0 and info["max_blocks_per_sm"] >= 1
     for d in (64, 128):
         wide = fa.query_fused(d, 256)
         assert wide["rows_per_block"] == 256 and wide["waves_per_block"] == 8 and wide["block_size"] == 512
