@@ -1061,32 +1061,14 @@ __global__ __launch_bounds__(64 * kGroups * kWpg) void fused_attention_kernel(co
         static_assert(kRecords * kRec * 4 + kGroups * kWpg * kObuf * 2 <= (C::kLdsElems + C::kQElems) * 2,
                       "records and store staging fit the LDS array");
         float* const recs = reinterpret_cast<float*>(lds);
-        // Holders: A = [0, a_hi], B = [b_lo, b_hi]; g_cross holds both.
-        int g_cross = kGroups, a_hi = -1, b_lo = kGroups, b_hi = -1;
-#pragma unroll
-        for (int g = 0; g < kGroups; ++g)
-        {
-            const int g0 = split.first[g];
-            const int gc = split.count[g];
-            if (gc > 0 && g0 < e_tiles) a_hi = g;
-            if (gc > 0 && g0 + gc > e_tiles)
-            {
-                b_lo = min(b_lo, g);
-                b_hi = g;
-            }
-            if (g0 < e_tiles && e_tiles < g0 + gc) g_cross = g;
-        }
+        const fa::FusedListHolders holders = fa::fused_list_holders(split, e_tiles);
+        const int g_cross = holders.cross, a_hi = holders.a_hi, b_lo = holders.b_lo, b_hi = holders.b_hi;
+        static_assert(kRecords == kWpg * (kGroups + 1), "record numbering");
         // The record of holder g's partial of half block `half`.
         auto record = [&](int g, int half, int w) {
-            const int part = (half == 1 && g == g_cross) ? 1 : 0;
-            return recs + ((g + part + (g_cross < g ? 1 : 0)) * kWpg + w) * kRec;
+            return recs + fa::fused_list_record(holders, g, half, w, kWpg) * kRec;
         };
-        // Finaliser of head-dim half dh of half block `half` (a lone holder
-        // takes both halves).
-        auto finaliser = [&](int half, int dh) {
-            if (half == 0) return a_hi == 0 ? 0 : dh;
-            return b_hi == b_lo ? b_hi : b_hi - 1 + dh;
-        };
+        auto finaliser = [&](int half, int dh) { return fa::fused_list_finaliser(holders, half, dh); };
         auto put_half = [&](float* r, const f32x16 (&oo)[D / 32], int dh) {
 #pragma unroll
             for (int r4 = 0; r4 < 4; ++r4)

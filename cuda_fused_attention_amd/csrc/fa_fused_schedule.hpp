@@ -102,4 +102,57 @@ FA_HD inline FusedSplit fused_split(int n_tiles) { return fused_split_n(n_tiles,
 // One wave group (no split of the KV range): group 0 takes every tile.
 FA_HD inline FusedSplit fused_single(int n_tiles) { return fused_split_n(n_tiles, 1); }
 
+// The list layout's merge bookkeeping. The workgroup's work list is the K/V
+// tiles of half block A (items [0, e_items)) followed by those of half block
+// B; the split gives each group a contiguous range of items. The holders of
+// a half block are the groups whose range covers some of its items: A's are
+// [0, a_hi], B's [b_lo, b_hi]; at most one group (cross) covers both, and it
+// then holds two partials. Each head-dim half dh of a half block's rows is
+// finalised by one holder: a lone holder takes both halves, otherwise groups
+// 0 and 1 finalise A and the last two holders B, so no group finalises both
+// half blocks (whenever a group crosses, every group has items and B's last
+// holder is the last group).
+struct FusedListHolders
+{
+    int cross;  // the group holding partials of both half blocks, or groups
+    int a_hi;   // A's holders are groups [0, a_hi] (-1: none)
+    int b_lo;   // B's holders are groups [b_lo, b_hi] (b_hi -1: none)
+    int b_hi;
+};
+
+FA_HD inline FusedListHolders fused_list_holders(const FusedSplit& s, int e_items)
+{
+    FusedListHolders r{s.groups, -1, s.groups, -1};
+    for (int g = 0; g < s.groups; ++g)
+    {
+        const int g0 = s.first[g];
+        const int gc = s.count[g];
+        if (gc > 0 && g0 < e_items) r.a_hi = g;
+        if (gc > 0 && g0 + gc > e_items)
+        {
+            if (r.b_lo > g) r.b_lo = g;
+            r.b_hi = g;
+        }
+        if (g0 < e_items && e_items < g0 + gc) r.cross = g;
+    }
+    return r;
+}
+
+// Finaliser of head-dim half dh of half block `half` (0: A, 1: B).
+FA_HD inline int fused_list_finaliser(const FusedListHolders& h, int half, int dh)
+{
+    if (half == 0) return h.a_hi == 0 ? 0 : dh;
+    return h.b_hi == h.b_lo ? h.b_hi : h.b_hi - 1 + dh;
+}
+
+// Merge record of group g's partial of half block `half` for the wave with
+// slot index w of `waves` per group: records are numbered in list order
+// (the crossing group's two partials take two consecutive numbers), so at
+// most waves * (groups + 1) records exist.
+FA_HD inline int fused_list_record(const FusedListHolders& h, int g, int half, int w, int waves)
+{
+    const int part = (half == 1 && g == h.cross) ? 1 : 0;
+    return (g + part + (h.cross < g ? 1 : 0)) * waves + w;
+}
+
 }  // namespace fa

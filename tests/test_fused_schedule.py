@@ -166,3 +166,98 @@ def test_schedule_checker_catches_a_short_pipeline(tmp_path):
         out = subprocess.run([str(exe)], capture_output=True, text=True)
         assert out.returncode != 0 and out.stdout.strip() != "0", (i, out.stdout)
 
+
+
+LIST_PROGRAM = r'''
+#include "fa_fused_schedule.hpp"
+#include <cstdio>
+#include <set>
+using namespace fa;
+
+int main() {
+    long bad = 0;
+    const int G = 4, W = 2;
+    for (int e = 0; e <= 160; ++e)
+    for (int l = 0; l <= 160; ++l) {
+        if (e + l == 0) continue;
+        const FusedSplit s = fused_split_n(e + l, G);
+        const FusedListHolders h = fused_list_holders(s, e);
+        // holders are exactly the groups whose items meet the half block
+        auto covers = [&](int g, int half) {
+            const int lo = s.first[g], hi = s.first[g] + s.count[g];
+            return s.count[g] > 0 && (half == 0 ? lo < e : hi > e);
+        };
+        int crossing = 0;
+        for (int g = 0; g < G; ++g) {
+            const bool a = covers(g, 0), b = covers(g, 1);
+            if (a != (g <= h.a_hi)) ++bad;
+            if (b != (g >= h.b_lo && g <= h.b_hi)) ++bad;
+            if (a && b) { ++crossing; if (h.cross != g) ++bad; }
+        }
+        if (crossing > 1 || (crossing == 0 && h.cross != G)) ++bad;
+        if ((e > 0) != (h.a_hi >= 0) || (l > 0) != (h.b_hi >= 0)) ++bad;
+        // finalisers: holders of the half block; one each dim half; a lone
+        // holder takes both; no group finalises both half blocks
+        std::set<int> fin[2];
+        for (int half = 0; half < 2; ++half) {
+            const int lo = half == 0 ? 0 : h.b_lo, hi = half == 0 ? h.a_hi : h.b_hi;
+            if (hi < 0) continue;
+            for (int dh = 0; dh < 2; ++dh) {
+                const int f = fused_list_finaliser(h, half, dh);
+                if (f < lo || f > hi) ++bad;
+                fin[half].insert(f);
+            }
+            if ((lo == hi) != (fin[half].size() == 1)) ++bad;
+        }
+        for (int f : fin[0]) if (fin[1].count(f)) ++bad;
+        // records: distinct and inside the W * (G + 1) reserved
+        std::set<int> rec;
+        for (int g = 0; g < G; ++g)
+            for (int half = 0; half < 2; ++half) {
+                if (!covers(g, half)) continue;
+                for (int w = 0; w < W; ++w) {
+                    const int r = fused_list_record(h, g, half, w, W);
+                    if (r < 0 || r >= W * (G + 1) || !rec.insert(r).second) ++bad;
+                }
+            }
+    }
+    std::printf("%ld\n", bad);
+    return bad != 0;
+}
+'''
+
+
+def _run_list_program(tmp_path, prog, tag):
+    src = tmp_path / f"list_{tag}.cpp"
+    src.write_text(prog)
+    exe = tmp_path / f"list_{tag}"
+    r = subprocess.run(["g++", "-std=c++17", "-O1", f"-I{CSRC}", str(src), "-o", str(exe)], capture_output=True,
+                       text=True)
+    assert r.returncode == 0, r.stderr
+    return subprocess.run([str(exe)], capture_output=True, text=True)
+
+
+def test_list_layout_merge_bookkeeping(tmp_path):
+    """The list layout's merge plan (csrc/fa_fused_schedule.hpp, used by the
+    kernel), for every pair of half-block tile counts up to 160 with four
+    groups: the holders of each half block are exactly the groups whose items
+    meet it, at most one group holds both, every dim half has one finaliser
+    among the holders (a lone holder takes both), no group finalises both half
+    blocks, and the records of all partials are distinct and within the
+    reserved count."""
+    out = _run_list_program(tmp_path, LIST_PROGRAM, "ok")
+    assert out.returncode == 0 and out.stdout.strip() == "0", out.stdout + out.stderr
+
+
+def test_list_bookkeeping_checker_catches_mistakes(tmp_path):
+    """Planted in the checked header's use: numbering records without the
+    crossing group's extra slot collides records; B finalised by its first two
+    holders lets a crossing group finalise both half blocks."""
+    plants = [("const int r = fused_list_record(h, g, half, w, W);",
+               "const int r = (g + (half == 1 && g == h.cross ? 1 : 0)) * W + w;"),
+              ("const int f = fused_list_finaliser(h, half, dh);",
+               "const int f = half == 0 ? fused_list_finaliser(h, half, dh) : (lo == hi ? hi : lo + dh);")]
+    for i, (old, new) in enumerate(plants):
+        assert old in LIST_PROGRAM
+        out = _run_list_program(tmp_path, LIST_PROGRAM.replace(old, new), f"bad{i}")
+        assert out.returncode != 0 and out.stdout.strip() != "0", (i, out.stdout)
