@@ -68,6 +68,14 @@
 //     number of (row, key) pairs instead of the last one carrying a full
 //     dense row of tiles; within each SIMD one wave holds early rows and one
 //     late rows. Larger grids keep whole blocks, issued heaviest first.
+//   * List layout (kList; head_dim 64, causal grids of one round): the
+//     workgroup's two 64-row half blocks' K/V tiles form one list (the first
+//     half block's tiles, then the second's), split into four contiguous
+//     quarters walked by four groups of two waves. A group whose quarter
+//     crosses into the second half block sets its partial aside and moves to
+//     those rows, so every group computes on every step and each SIMD keeps
+//     two busy waves; the partials merge through LDS at the end (the plan:
+//     fused_list_holders / fused_list_finaliser / fused_list_record).
 //   * Workgroup ids are remapped so that all query blocks of a (batch, head)
 //     slab run on one XCD and share its L2 (measured: K and V are read from
 //     HBM once).
