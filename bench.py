@@ -30,6 +30,7 @@ from __future__ import annotations
 
 import argparse
 import hashlib
+import re
 import json
 import os
 import sys
@@ -57,16 +58,30 @@ EXTRA_WORKLOADS = ("c2", "c2_causal", "headline", "c3")
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
 # The sources that define the fused kernel's code: profiles/traffic.json
 # records their hash next to each counter measurement, and a measurement
-# taken on other sources is reported as stale (traffic null).
+# taken on other code is reported as stale (traffic null). The hash covers
+# the C++ sources with their comments removed and the device compiler flags,
+# so a change to comments alone keeps a measurement valid.
 KERNEL_SOURCES = ("cuda_fused_attention_amd/csrc/fa_fused.hip", "cuda_fused_attention_amd/csrc/fa_fused_schedule.hpp",
-                  "cuda_fused_attention_amd/csrc/fa_common.hpp", "cuda_fused_attention_amd/_build.py")
+                  "cuda_fused_attention_amd/csrc/fa_common.hpp")
+
+
+def strip_cpp_comments(text: str) -> str:
+    """C++ source without // and /* */ comments and with each line's
+    surrounding whitespace and the blank lines dropped (the kernel sources
+    hold no string literal with comment markers)."""
+    text = re.sub(r"/\*.*?\*/", " ", text, flags=re.S)
+    text = re.sub(r"//[^\n]*", "", text)
+    return "\n".join(line.strip() for line in text.splitlines() if line.strip())
 
 
 def kernel_source_sha() -> str:
+    from cuda_fused_attention_amd import _build
+
     h = hashlib.sha256()
     for rel in KERNEL_SOURCES:
-        with open(os.path.join(ROOT, rel), "rb") as fh:
-            h.update(rel.encode() + b"\0" + fh.read() + b"\0")
+        with open(os.path.join(ROOT, rel), encoding="utf-8") as fh:
+            h.update(rel.encode() + b"\0" + strip_cpp_comments(fh.read()).encode() + b"\0")
+    h.update(repr(_build.HIP_FLAGS).encode())
     return h.hexdigest()[:16]
 
 

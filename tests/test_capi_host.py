@@ -233,3 +233,17 @@ int main() {
                     "-lfa_mi355x", f"-Wl,-rpath,{pkg}"], check=True, capture_output=True)
     res = subprocess.run([str(exe)], capture_output=True, text=True)
     assert res.returncode == 0 and res.stdout.split() == ["0"], (res.stdout, res.stderr)
+
+
+def test_traffic_record_hash_ignores_comments_only():
+    """bench.py ties each HBM-traffic measurement (profiles/traffic.json) to
+    a hash of the fused kernel's code: comments and blank lines do not
+    change it; code and compiler flags do."""
+    import bench
+
+    code = "int a = 1;\nfloat f(float x) { return x * 2.0f; }\n"
+    noted = "// note\nint a = 1;  /* old value 2\n */\n\nfloat f(float x) { return x * 2.0f; }  // doubled\n"
+    assert bench.strip_cpp_comments(code) == bench.strip_cpp_comments(noted)
+    assert bench.strip_cpp_comments(code) != bench.strip_cpp_comments(code.replace("2.0f", "3.0f"))
+    sha = bench.kernel_source_sha()
+    assert len(sha) == 16 and int(sha, 16) >= 0
