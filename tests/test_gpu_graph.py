@@ -49,6 +49,25 @@ def test_fused_launch_replays_in_a_graph(fa, oracle_mod, B, H, N, D, causal):
     _capture_and_replay(fa, launch, q, eager)
 
 
+def test_pinned_configurations_replay_in_a_graph(fa, oracle_mod):
+    """Every pinned fused configuration at head_dim 64 (the four-group ones,
+    the list layout's moving waves and LDS merge included), captured and
+    replayed, causal and dense."""
+    B, H, N, D = 2, 3, 1000, 64
+    qb, kb, vb = oracle_mod.make_inputs(B, H, N, D, seeds={"q": 64, "k": 65, "v": 66})
+    q, k, v = to_dev(qb), to_dev(kb), to_dev(vb)
+    shape = fa.AttentionShape(B, H, N, D)
+    for name, (rows, groups) in fa.FUSED_CONFIGS.items():
+        for causal in (True, False):
+            eager = from_dev(run(fa, name, q, k, v, causal))
+            say("graph pinned", name, causal)
+
+            def launch(o, stream, rows=rows, groups=groups, causal=causal):
+                assert fa.launch_attention_fused_groups(q, k, v, o, shape, causal, rows, groups, stream=stream)
+
+            _capture_and_replay(fa, launch, q, eager)
+
+
 def test_unfused_launch_replays_in_a_graph(fa, oracle_mod):
     import torch
 

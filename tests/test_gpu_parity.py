@@ -231,28 +231,30 @@ def test_v3_picks_the_configuration_by_grid(fa, oracle_mod):
 
 
 def test_deterministic(fa, oracle_mod):
-    q, k, v = (to_dev(x) for x in oracle_mod.make_inputs(2, 4, 1000, 128))
-    for kernel in kernels_for(128):
-        for causal in (False, True):
-            say("determinism", kernel, causal)
-            a = from_dev(run(fa, kernel, q, k, v, causal))
-            b = from_dev(run(fa, kernel, q, k, v, causal))
-            assert np.array_equal(a, b)
+    for D in (64, 128):
+        q, k, v = (to_dev(x) for x in oracle_mod.make_inputs(2, 4, 1000, D))
+        for kernel in kernels_for(D):
+            for causal in (False, True):
+                say("determinism", kernel, D, causal)
+                a = from_dev(run(fa, kernel, q, k, v, causal))
+                b = from_dev(run(fa, kernel, q, k, v, causal))
+                assert np.array_equal(a, b)
 
 
 def test_non_default_stream(fa, oracle_mod):
     import torch
 
-    q, k, v = oracle_mod.make_inputs(1, 2, 257, 128)
-    ref = oracle_mod.attention(q, k, v, True)
     s = torch.cuda.Stream()
-    qd, kd, vd = to_dev(q), to_dev(k), to_dev(v)
-    torch.cuda.synchronize()
-    for kernel in kernels_for(128):
-        say("stream", kernel)
-        with torch.cuda.stream(s):
-            o = run(fa, kernel, qd, kd, vd, True, stream=s)
-        check(oracle_mod, from_dev(o), ref, f"stream {kernel}")
+    for D in (64, 128):
+        q, k, v = oracle_mod.make_inputs(1, 2, 257, D)
+        ref = oracle_mod.attention(q, k, v, True)
+        qd, kd, vd = to_dev(q), to_dev(k), to_dev(v)
+        torch.cuda.synchronize()
+        for kernel in kernels_for(D):
+            say("stream", kernel, D)
+            with torch.cuda.stream(s):
+                o = run(fa, kernel, qd, kd, vd, True, stream=s)
+            check(oracle_mod, from_dev(o), ref, f"stream {kernel} D={D}")
 
 
 def test_v0_profile_bitwise_equal(fa, oracle_mod):
