@@ -613,7 +613,7 @@ __global__ __launch_bounds__(64 * kGroups * kWpg) void fused_attention_kernel(co
         // loop (four copies overflow the instruction cache).
         const int G = gtag;
         // LDS byte addresses of this group's K and V stages (DMA targets):
-        // the array's base plus compile-time offsets.
+        // the array's base plus the group's offset (uniform, in SGPRs).
         const uint32_t k_lds = lds_base + G * C::kGroupElems * 2;
         const uint32_t v_lds = k_lds + kStages * C::kTileElems * 2;
         int tb = 0, cnt = 0;  // this group's list items [tb, tb + cnt)
@@ -666,8 +666,9 @@ __global__ __launch_bounds__(64 * kGroups * kWpg) void fused_attention_kernel(co
 
         // DMA lane offsets (full tiles and the tail tile) and copy helpers.
         // Every copy point issues a fixed number of copies so the vmcnt
-        // waits below are constants. A tile index past the end is clamped to
-        // the last tile; such a copy lands in a stage nobody reads again.
+        // waits below are constants. An item past the end of the list is
+        // clamped to the last one; such a copy lands in a stage nobody reads
+        // again.
         uint32_t koff[C::kIssues], voff[C::kIssues];
         dma_lane_offsets<D, kWpg, false>(wg, lane, koff);
         dma_lane_offsets<D, kWpg, true>(wg, lane, voff);
@@ -986,7 +987,7 @@ __global__ __launch_bounds__(64 * kGroups * kWpg) void fused_attention_kernel(co
 #pragma unroll
             for (int u = 0; u < C::kIssues; ++u) copy_v(jj + fa::kFusedVAhead, (stage + fa::kFusedVAhead) % kStages, u);
         }
-        // Pad to the common barrier count of both groups.
+        // Pad to the common barrier count of all groups.
         for (int b = fa::fused_group_barriers(G, cnt); b < split.barriers; ++b) barrier();
         // Drain this wave's last (unused) copies before LDS is reused below.
         wait_vm_lgkm0<0>();
