@@ -11,7 +11,7 @@ slab the kernel skips fails the check."""
 import numpy as np
 import pytest
 
-from gpu_common import from_dev, nan_like, run, say
+from gpu_common import from_dev, nan_like, run, say, to_dev
 from test_gpu_parity import check, fa  # noqa: F401 (fa: fixture)
 
 pytestmark = [pytest.mark.gpu, pytest.mark.slow]
@@ -39,3 +39,24 @@ def test_tensors_past_4_gib(fa, oracle_mod):
                 check(oracle_mod, got, refs[s], f"large {kernel} causal={causal} slab {s}")
             del o
             torch.cuda.empty_cache()
+
+
+def test_list_layout_long_sequence(fa, oracle_mod):
+    """(1,2,16384,64) causal is one round of 128-row workgroups (2 slabs x
+    128 blocks = 256), so v3 runs the list layout: each workgroup's two half
+    blocks are far apart in length (the first pair's tile lists are 2 and 512
+    long), so quarters cross from the early to the late half block at every
+    position. Every row of both slabs against the FP64 oracle, for v3 and the
+    pinned configuration (bitwise equal)."""
+    B, H, N, D = 1, 2, 16384, 64
+    cus = fa.query_tensorcore_v3(64)["compute_units"]
+    qb, kb, vb = oracle_mod.make_inputs(B, H, N, D, seeds={"q": 91, "k": 92, "v": 93})
+    ref = oracle_mod.attention(qb, kb, vb, True)
+    say("list long", B, H, N, D)
+    if cus == 256:
+        assert fa.tensorcore_v3_config(fa.AttentionShape(B, H, N, D), True) == (128, 4)
+    got = from_dev(run(fa, "v3_mfma", *(to_dev(x) for x in (qb, kb, vb)), True))
+    check(oracle_mod, got, ref, "list long v3")
+    pinned = from_dev(run(fa, "v3_128x4", *(to_dev(x) for x in (qb, kb, vb)), True))
+    assert cus != 256 or np.array_equal(got, pinned)
+    check(oracle_mod, pinned, ref, "list long pinned")
