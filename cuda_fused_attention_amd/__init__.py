@@ -230,7 +230,8 @@ def tensorcore_v3b_hbm_bytes(shape, causal: bool) -> float:
 
 
 def tensorcore_v3_rows_per_block(shape, causal: bool) -> int:
-    """Query rows per workgroup the v3 entry runs at this shape (64, 128 or 256)."""
+    """Query rows per workgroup the v3 entry runs at this shape (64, 128 or 256;
+    tensorcore_v3_config also gives the KV groups)."""
     s = _shape_of(shape)
     return int(lib().fa_tensorcore_v3_rows_per_block(s.batch, s.heads, s.seq_len, s.head_dim, int(causal)))
 

@@ -165,8 +165,8 @@ int fa_launch_attention_fused_groups(const void* q, const void* k, const void* v
 
 /* No counterpart in the reference: fa_query_tensorcore_v3 for the
  * configuration fa_launch_attention_fused runs with rows_per_block (64, 128
- * or 256), or fa_launch_attention_fused_groups with (rows_per_block,
- * kv_groups). agprs_per_thread comes from the compiler's resource report of
+ * or 256; two groups below 256 rows), or fa_launch_attention_fused_groups
+ * with (rows_per_block, kv_groups). agprs_per_thread comes from the compiler's resource report of
  * the kernel, recorded when the library was built. */
 int fa_query_fused(int head_dim, int rows_per_block, fa_tiling_info* info);
 int fa_query_fused_groups(int head_dim, int rows_per_block, int kv_groups, fa_tiling_info* info);
