@@ -17,6 +17,8 @@
 //
 // Usage: bench_flash_attention [--quick | --accuracy-only] [output_directory]
 //        bench_flash_attention --v0-profile [--check] [output_directory]
+//        bench_flash_attention --v0-profile B H N D causal [samples [warmup]] [output_directory]
+//        bench_flash_attention --v0-profile --profiler B H N D causal [iterations]
 //   --quick          B = 1, N in {512, 2048} only (eight grid cases).
 //   --accuracy-only  the accuracy suite alone (the ctest).
 //   --v0-profile     the v0 stage profile (benchmarks/profile_attention_v0.cu):
@@ -28,7 +30,13 @@
 //                    unmarked v0 launch, written as v0_stage_timing.csv with
 //                    the reference's columns. With --check: the bitwise
 //                    checks alone, at N in {1, 17, 256}, D in {64, 128},
-//                    dense and causal.
+//                    dense and causal. With a shape: that shape alone (its
+//                    samples and warmups as given, 30 and 5 by default).
+//                    With --profiler and a shape: only `iterations` (default
+//                    1) instrumented launches without events, no check and no
+//                    warmup, for a profiler run (rocprofv3 --kernel-trace
+//                    sees one QK, softmax and PV kernel per iteration; the
+//                    reference's --ncu mode, profile_attention_v0.cu:195-197).
 // Exit status: 0 when every accuracy row passes both gates and every timed
 // output is finite, 1 otherwise, 2 on a usage or HIP error.
 
@@ -236,7 +244,8 @@ double quantile_of(std::vector<double> xs, double p)
 // One v0 stage-profile shape: bitwise check of the instrumented launch
 // against the plain one, then (unless check_only) the stage timings.
 // Returns false on a mismatch.
-bool v0_profile_shape(const fa::AttentionShape& s, bool causal, bool check_only, std::ostream* csv)
+bool v0_profile_shape(const fa::AttentionShape& s, bool causal, bool check_only, std::ostream* csv,
+                      int samples = 30, int warmup = kWarmup)
 {
     const size_t n = elements(s);
     std::vector<uint16_t> host(n), plain(n), got(n);
@@ -275,8 +284,7 @@ bool v0_profile_shape(const fa::AttentionShape& s, bool causal, bool check_only,
                 causal ? 1 : 0, same ? "PASS (finite, bitwise equal to v0)" : "FAIL");
     if (same && !check_only)
     {
-        constexpr int kSamples = 30;
-        for (int i = 0; i < kWarmup; ++i)
+        for (int i = 0; i < warmup; ++i)
         {
             fa::launch_attention_unfused(q.bf16(), k.bf16(), v.bf16(), o.bf16(), wsp, s, causal, stream);
             HIP_OK(fa::launch_attention_unfused_profile(q.bf16(), k.bf16(), v.bf16(), o.bf16(), wsp, s, causal,
@@ -285,7 +293,7 @@ bool v0_profile_shape(const fa::AttentionShape& s, bool causal, bool check_only,
         HIP_OK(hipGetLastError());
         HIP_OK(hipStreamSynchronize(stream));
         std::vector<double> t[5];
-        for (int i = 0; i < kSamples; ++i)
+        for (int i = 0; i < samples; ++i)
         {
             // an unmarked v0 launch between its own events, then the instrumented one
             HIP_OK(hipEventRecord(ev[4], stream));
@@ -329,27 +337,68 @@ bool v0_profile_shape(const fa::AttentionShape& s, bool causal, bool check_only,
     return same;
 }
 
+// The profiler mode: `iterations` instrumented v0 launches with no events,
+// no validation and no warmup, so a profiler sees exactly those kernels.
+bool v0_profile_launches(const fa::AttentionShape& s, bool causal, int iterations)
+{
+    const size_t n = elements(s);
+    std::vector<uint16_t> host(n);
+    DeviceBuffer q(n * 2), k(n * 2), v(n * 2), o(n * 2), ws(std::max<size_t>(4, fa::unfused_workspace_bytes(s)));
+    fa_oracle_fill_normal_mt19937(host.data(), static_cast<int64_t>(n), 11u);
+    HIP_OK(hipMemcpy(q.ptr, host.data(), n * 2, hipMemcpyHostToDevice));
+    fa_oracle_fill_normal_mt19937(host.data(), static_cast<int64_t>(n), 22u);
+    HIP_OK(hipMemcpy(k.ptr, host.data(), n * 2, hipMemcpyHostToDevice));
+    fa_oracle_fill_normal_mt19937(host.data(), static_cast<int64_t>(n), 33u);
+    HIP_OK(hipMemcpy(v.ptr, host.data(), n * 2, hipMemcpyHostToDevice));
+    for (int i = 0; i < iterations; ++i)
+        HIP_OK(fa::launch_attention_unfused_profile(q.bf16(), k.bf16(), v.bf16(), o.bf16(),
+                                                    static_cast<float*>(ws.ptr), s, causal, nullptr, nullptr));
+    HIP_OK(hipDeviceSynchronize());
+    std::vector<uint16_t> got(n);
+    HIP_OK(hipMemcpy(got.data(), o.ptr, n * 2, hipMemcpyDeviceToHost));
+    size_t nan = 0, inf = 0;
+    count_nonfinite(got, nan, inf);
+    std::printf("v0 profiler launches B=%d H=%d N=%d D=%d causal=%d: %d iteration(s), output %s\n", s.batch, s.heads,
+                s.seq_len, s.head_dim, causal ? 1 : 0, iterations, nan == 0 && inf == 0 ? "finite" : "NOT finite");
+    return nan == 0 && inf == 0;
+}
+
 }  // namespace
 
 int main(int argc, char** argv)
 {
-    bool quick = false, accuracy_only = false, v0_profile = false, check_only = false;
+    bool quick = false, accuracy_only = false, v0_profile = false, check_only = false, profiler = false;
     std::filesystem::path out_dir = "results/raw/flash_attention";
+    std::vector<int> numbers;  // --v0-profile shape: B H N D causal [samples [warmup] | iterations]
+    auto usage = [&](int status) {
+        std::printf("usage: %s [--quick | --accuracy-only] [output_directory]\n"
+                    "       %s --v0-profile [--check] [output_directory]\n"
+                    "       %s --v0-profile B H N D causal [samples [warmup]] [output_directory]\n"
+                    "       %s --v0-profile --profiler B H N D causal [iterations]\n",
+                    argv[0], argv[0], argv[0], argv[0]);
+        return status;
+    };
     for (int a = 1; a < argc; ++a)
     {
         const std::string arg = argv[a];
+        char* end = nullptr;
+        const long value = std::strtol(arg.c_str(), &end, 10);
         if (arg == "--quick") quick = true;
         else if (arg == "--accuracy-only") accuracy_only = true;
         else if (arg == "--v0-profile") v0_profile = true;
         else if (arg == "--check") check_only = true;
-        else if (arg == "--help" || arg == "-h" || arg.rfind("--", 0) == 0)
-        {
-            std::printf("usage: %s [--quick | --accuracy-only] [output_directory]\n"
-                        "       %s --v0-profile [--check] [output_directory]\n", argv[0], argv[0]);
-            return arg.rfind("--h", 0) == 0 || arg == "-h" ? 0 : 2;
-        }
+        else if (arg == "--profiler") profiler = true;
+        else if (arg == "--help" || arg == "-h") return usage(0);
+        else if (arg.rfind("--", 0) == 0) return usage(2);
+        else if (v0_profile && !arg.empty() && *end == '\0' && value >= 0 && value <= 1 << 30)
+            numbers.push_back(static_cast<int>(value));
         else out_dir = arg;
     }
+    const size_t max_numbers = profiler ? 6 : 7;
+    if (!numbers.empty() && (numbers.size() < 5 || numbers.size() > max_numbers || check_only)) return usage(2);
+    if (profiler && numbers.empty()) return usage(2);
+    if (!numbers.empty() && (numbers[0] < 1 || numbers[1] < 1 || numbers[2] < 1 || numbers[3] < 1 || numbers[4] > 1))
+        return usage(2);
     std::error_code ec;
     std::filesystem::create_directories(out_dir, ec);
     if (ec)
@@ -361,11 +410,20 @@ int main(int argc, char** argv)
     {
         bool ok = true;
         std::ofstream stage_csv;
-        if (!check_only)
+        if (!check_only && !profiler)
             stage_csv = open_csv(out_dir / "v0_stage_timing.csv",
                                  "shape,batch,heads,seq_len,head_dim,causal,metric,median_ms,q1_ms,q3_ms,iqr_ms,"
                                  "share_of_pipeline");
-        if (check_only)
+        if (!numbers.empty())
+        {
+            const fa::AttentionShape shape{numbers[0], numbers[1], numbers[2], numbers[3]};
+            const bool causal = numbers[4] != 0;
+            if (profiler) ok = v0_profile_launches(shape, causal, numbers.size() > 5 ? std::max(1, numbers[5]) : 1);
+            else
+                ok = v0_profile_shape(shape, causal, false, &stage_csv, numbers.size() > 5 ? std::max(1, numbers[5]) : 30,
+                                      numbers.size() > 6 ? numbers[6] : kWarmup);
+        }
+        else if (check_only)
         {
             for (int n : {1, 17, 256})
                 for (int d : {64, 128})

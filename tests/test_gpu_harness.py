@@ -60,3 +60,30 @@ def test_harness_quick(tmp_path):
     fields, raw = rows(tmp_path / "raw_timings.csv")
     assert fields == RAW
     assert len(raw) == 8 * 3 * 30
+
+
+def test_v0_profile_modes(tmp_path):
+    """The v0 stage profile's other two modes (benchmarks/profile_attention_v0.cu:
+    195-197): one shape with its own sample and warmup counts (a stage-timing
+    CSV with the reference's columns and five metrics), and the profiler mode
+    (plain instrumented launches without events or checks, for rocprofv3)."""
+    if not os.path.exists(BINARY):
+        pytest.fail(f"{BINARY} is missing: run __graft_entry__.build()")
+    print("harness --v0-profile shape", flush=True)
+    run = subprocess.run([BINARY, "--v0-profile", "1", "2", "300", "64", "1", "4", "1", str(tmp_path)],
+                         capture_output=True, text=True, timeout=120)
+    assert run.returncode == 0, run.stdout[-2000:] + run.stderr[-2000:]
+    assert "PASS (finite, bitwise equal to v0)" in run.stdout
+    fields, stage = rows(tmp_path / "v0_stage_timing.csv")
+    assert fields == ("shape,batch,heads,seq_len,head_dim,causal,metric,median_ms,q1_ms,q3_ms,iqr_ms,"
+                      "share_of_pipeline").split(",")
+    assert [r["metric"] for r in stage] == ["QK", "softmax", "PV", "instrumented_pipeline", "original_v0_e2e"]
+    assert all(r["shape"] == "b1h2n300d64_causal" and float(r["median_ms"]) > 0 for r in stage)
+
+    print("harness --v0-profile --profiler", flush=True)
+    run = subprocess.run([BINARY, "--v0-profile", "--profiler", "1", "2", "300", "64", "0", "3"],
+                         capture_output=True, text=True, timeout=120)
+    assert run.returncode == 0, run.stdout[-2000:] + run.stderr[-2000:]
+    assert "3 iteration(s), output finite" in run.stdout
+    bad = subprocess.run([BINARY, "--v0-profile", "--profiler"], capture_output=True, text=True, timeout=60)
+    assert bad.returncode == 2
