@@ -233,6 +233,12 @@ __device__ __forceinline__ i32x4 make_rsrc(ScalarPtr base, uint32_t offset, uint
 // one wait state between its write and the load.
 __device__ __forceinline__ void dma16(i32x4 rsrc, uint32_t voff, uint32_t lds)
 {
+    // rsrc must reach the asm in SGPRs: where the compiler cannot prove a
+    // descriptor uniform it keeps it in VGPRs and passes that tuple to the
+    // "s" operand, and the assembler rejects the copy ("invalid operand"), a
+    // build error. Every descriptor here is built from uniform values; a
+    // readfirstlane of each word would guard against it at two scalar moves
+    // per step in the two-group loop.
     lds = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(lds)));
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
