@@ -120,6 +120,13 @@ def test_argument_validation_before_launch(fa_lib):
     # unsupported head_dim: nothing launched, FA_ERROR_UNSUPPORTED
     assert L.fa_launch_attention_tensorcore_v3(fake, fake, fake, fake, 1, 1, 64, 96, 0, None) == fa_lib.FA_ERROR_UNSUPPORTED
     assert L.fa_launch_attention_tensorcore_v3b(fake, fake, fake, fake, 1, 1, 64, 32, 1, None) == fa_lib.FA_ERROR_UNSUPPORTED
+    # the four-group configurations exist at head_dim 64 only; unknown
+    # (rows, groups) pairs are invalid
+    for rows, groups in ((64, 4), (128, 4)):
+        assert L.fa_launch_attention_fused_groups(fake, fake, fake, fake, 1, 1, 64, 128, 1, rows, groups,
+                                                  None) == fa_lib.FA_ERROR_UNSUPPORTED
+    for rows, groups in ((128, 1), (256, 2), (128, 3), (96, 4), (0, 2)):
+        assert L.fa_launch_attention_fused_groups(fake, fake, fake, fake, 1, 1, 64, 64, 0, rows, groups, None) == 1
     # empty shapes are a successful no-op
     assert L.fa_launch_attention_tensorcore_v3(None, None, None, None, 0, 8, 64, 64, 0, None) == 0
     assert L.fa_launch_attention_tensorcore_v3(None, None, None, None, 1, 8, 0, 128, 1, None) == 0
