@@ -1,0 +1,72 @@
+"""Seeded random shapes and a sweep of sequence lengths, against the FP64 oracle
+through the C ABI, every row compared (the comparator of
+benchmarks/bench_flash_attention.cu:183-213 plus BASELINE's 2^-7 row gate).
+
+The fixed cases elsewhere sit on tile multiples, the reference's boundary set
+(N <= 256) and the grid (multiples of 512). Here the lengths fall anywhere up
+to a few thousand keys, so the tail tile, the split of the key range between
+wave groups, the paired causal layout's half blocks and the list layout's
+crossing group all land at positions the fixed cases do not reach. Both sets
+are drawn once from fixed seeds, so a failure names a reproducible case.
+"""
+import numpy as np
+import pytest
+
+from gpu_common import HOST_THREADS, kernels_for, run_bits, say
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def fa(fa_lib):
+    import torch
+
+    if not torch.cuda.is_available():
+        pytest.fail("GPU tests need a visible MI355X")
+    return fa_lib
+
+
+def random_shapes(count, seed):
+    """(B, H, N, D, causal): B 1-3, H 1-5; N log-uniform in [1, 256) for a
+    third of the shapes, uniform in [256, 2600] for the rest."""
+    rng = np.random.default_rng(seed)
+    shapes = []
+    for i in range(count):
+        n = int(np.exp(rng.uniform(0.0, np.log(256.0)))) if i % 3 == 0 else int(rng.integers(256, 2601))
+        shapes.append((int(rng.integers(1, 4)), int(rng.integers(1, 6)), max(1, n), int(rng.choice([64, 128])),
+                       bool(rng.integers(0, 2))))
+    return shapes
+
+
+RANDOM_SHAPES = random_shapes(30, seed=20261202)
+
+
+def test_random_shapes(fa, oracle_mod):
+    """Every kernel that supports the head dim (v0 and each fused
+    configuration) on each shape; inputs uniform [-1, 1) from per-shape seeds."""
+    for idx, (B, H, N, D, causal) in enumerate(RANDOM_SHAPES):
+        q, k, v = oracle_mod.make_inputs(B, H, N, D, seeds={"q": 100 + idx, "k": 200 + idx, "v": 300 + idx})
+        ref = oracle_mod.attention(q, k, v, causal, threads=HOST_THREADS)
+        for kernel in kernels_for(D):
+            say("random shape", idx, kernel, B, H, N, D, causal)
+            acc = oracle_mod.compare(run_bits(fa, kernel, q, k, v, causal), ref)
+            assert acc.passed, f"random shape {idx} {kernel} {(B, H, N, D, causal)}: {acc}"
+
+
+# One slab pair at head_dim 64: every length gives a one-round grid, so the
+# list layout pairs half blocks; the crossing group and its step move with N.
+LIST_SWEEP_N = [33, 97, 160, 255, 300, 511, 700, 777, 1023, 1100, 1234, 1500, 1537, 1663, 1777, 1888, 1999,
+                2047, 2111, 2300, 2500, 2600]
+
+
+def test_list_layout_length_sweep(fa, oracle_mod):
+    """The four-group list layout (pinned) and the v3 default, causal and
+    dense, at 22 lengths between 33 and 2600."""
+    for N in LIST_SWEEP_N:
+        q, k, v = oracle_mod.make_inputs(1, 2, N, 64, seeds={"q": N, "k": N + 1, "v": N + 2})
+        for causal in (True, False):
+            ref = oracle_mod.attention(q, k, v, causal, threads=HOST_THREADS)
+            for kernel in ("v3_128x4", "v3_mfma"):
+                say("list sweep", kernel, N, causal)
+                acc = oracle_mod.compare(run_bits(fa, kernel, q, k, v, causal), ref)
+                assert acc.passed, f"list sweep {kernel} N={N} causal={causal}: {acc}"
