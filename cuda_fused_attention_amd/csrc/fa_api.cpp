@@ -295,7 +295,7 @@ int fa_time_batch(int which, const void* q, const void* k, const void* v, void* 
 const char* fa_build_info(void)
 {
     return "libfa_mi355x gfx950: v0 unfused (fp32 SIMT, LDS-tiled) + fused v_mfma_f32_32x32x16_bf16 "
-           "(32 query rows/wave, 32-key K/V tiles by buffer-load LDS DMA, 4 stages per tensor, MFMA/VALU interleaved per wave; "
+           "(32 query rows/wave, 32-key K/V tiles by buffer-load LDS DMA, 3 stages per tensor, MFMA/VALU interleaved per wave; "
            "workgroups of 128 rows (2 split-KV groups x 4 waves), 64 rows (2 x 2, or 4 x 2 at head_dim 64) or "
            "256 rows (1 group x 8 waves), v3 picks by shape)";
 }

@@ -31,21 +31,21 @@
 //                MFMA pipe computes S^T of tile jj+1 (its K operands were
 //                read in the previous block B) while the VALU finishes tile
 //                jj's exponentials (second half); the wave issues its share
-//                of the DMA copies of K tile jj+4;
-//       barrier: wait until only the copies of steps jj-1 and jj are in
-//                flight and every LDS read has completed, workgroup barrier
-//                (the step's only one);
+//                of the DMA copies of K tile jj+3;
+//       barrier: wait until only block A's copies are in flight and every
+//                LDS read has completed, workgroup barrier (the step's only
+//                one);
 //       block B: the K operands of tile jj+2 are read; the MFMA pipe
 //                accumulates O^T += V^T P^T of tile jj while the VALU starts
 //                tile jj+1 (mask, first half of the exponentials) after
 //                checking tile jj's row sums;
-//                the wave issues its share of the copies of V tile jj+3.
+//                the wave issues its share of the copies of V tile jj+2.
 //     MFMA and VALU work of one wave are independent inside each block, so
 //     the compiler interleaves them within each chunk (scheduling fences
 //     keep the chunks apart), with one DMA issue per chunk; the other
 //     group's wave on the same SIMD fills the remaining gaps.
 //   * K and V tiles go HBM -> LDS directly with buffer_load_dwordx4 ... lds
-//     (lane l of an issue lands at M0 + 16*l), four stages per tensor per
+//     (lane l of an issue lands at M0 + 16*l), three stages per tensor per
 //     group. The LDS rows are row-major with the 16-byte chunk index
 //     XOR-swizzled per row so that every ds_read_b128 (K) and
 //     ds_read_b64_tr_b16 (V) phase hits distinct banks; the swizzle is
@@ -145,8 +145,22 @@ struct Cfg : TileCopy<D, kWpg>
     static constexpr int kThreads = 64 * kGroups * kWpg;
     static constexpr int kTileElems = kTileKV * D;                     // bf16 per K or V tile
     static constexpr int kGroupElems = 2 * kStages * kTileElems;       // one group's K and V stages
-    static constexpr int kLdsElems = kGroups * kGroupElems;
+    static constexpr int kStageElems = kGroups * kGroupElems;          // every group's stages
     static constexpr int kQElems = kSlots * 32 * D;                    // Q rows of the slots
+    // Once every copy has landed, the merge and the store reuse the array;
+    // bf16 elements they need ahead of the Q area (the kernel's merge code
+    // asserts each bound): one group: each wave's 32-row store staging;
+    // two groups: both directions of each slot's half-O^T exchange; four
+    // groups: that plus the hand-over of groups 2 and 3; the list layout:
+    // its records and store staging, which may also use the Q area.
+    static constexpr int kOtFloats = (D / 32) * 16 * 64;               // one wave's O^T
+    static constexpr int kXSlotFloats = 2 * ((D / 64) * 16 * 64 + 128);
+    static constexpr int kMergeElems =
+        kList ? (2 * (kGroups + 1) * (kOtFloats + 128) * 4 + kGroups * kWpg * 32 * D * 2) / 2 - kQElems
+        : kGroups == 1 ? kWpg * 32 * D
+        : kGroups == 2 ? kWpg * kXSlotFloats * 2
+                       : 2 * (kWpg * kXSlotFloats + 2 * kWpg * (kOtFloats + 128));
+    static constexpr int kLdsElems = kStageElems > kMergeElems ? kStageElems : kMergeElems;
     static constexpr int kQIssues = 32 * D * 2 / 1024;                 // DMA issues per slot's Q rows
     static constexpr int kQRowsPerIssue = 64 / (D / 8);                // rows one (64-lane) Q copy covers
     static constexpr int kQIssuesPerWave = kSlots * kQIssues / (kGroups * kWpg);
@@ -790,11 +804,11 @@ __global__ __launch_bounds__(64 * kGroups * kWpg) void fused_attention_kernel(co
         // the matrix pipe starts at the top of every chunk and the copies
         // trickle into the memory pipeline instead of stalling the wave in a
         // burst.
-        //   Block A: V operand reads of tile jj; copies of K tile jj+4;
+        //   Block A: V operand reads of tile jj; copies of K tile jj+3;
         //            S^T of tile jj+1 beside the second half of tile jj's
         //            exponentials.
         //   Block B: the check of tile jj's row sums; K operand reads of
-        //            tile jj+2; copies of V tile jj+3; O^T += V^T P^T of tile
+        //            tile jj+2; copies of V tile jj+2; O^T += V^T P^T of tile
         //            jj beside the first half of tile jj+1's exponentials.
         //
         // Exponentials use the current base; no per-tile row max is taken.
@@ -964,12 +978,12 @@ __global__ __launch_bounds__(64 * kGroups * kWpg) void fused_attention_kernel(co
             if (sw_step == 0) load_b_q();
         fa::fused_group_walk(n_active, [&](auto par_tag, int jj) {
             block_a(par_tag, jj);
-            // Only the copies of steps jj-1 and jj may still be in flight:
+            // Only block A's copies (K_{jj+3}) may still be in flight:
             // K_{jj+2} (read in block B) and V_{jj+1} (read in step jj+1)
             // have landed and become visible after the barrier; every LDS
             // read issued so far has completed, which frees the stages the
             // next copies overwrite.
-            wait_vm_lgkm0<3 * C::kIssues>();
+            wait_vm_lgkm0<fa::kFusedStepInFlight * C::kIssues>();
             barrier();
             block_b(par_tag, jj);
             if constexpr (kList)
@@ -988,7 +1002,7 @@ __global__ __launch_bounds__(64 * kGroups * kWpg) void fused_attention_kernel(co
             const int stage = jj % kStages;
 #pragma unroll
             for (int u = 0; u < C::kIssues; ++u) copy_k(jj + fa::kFusedKAhead, (stage + fa::kFusedKAhead) % kStages, u);
-            wait_vm_lgkm0<3 * C::kIssues>();
+            wait_vm_lgkm0<fa::kFusedStepInFlight * C::kIssues>();
             barrier();
 #pragma unroll
             for (int u = 0; u < C::kIssues; ++u) copy_v(jj + fa::kFusedVAhead, (stage + fa::kFusedVAhead) % kStages, u);
@@ -1422,7 +1436,7 @@ int launch_fused(const void* q, const void* k, const void* v, void* o, int batch
 //     prologue cost more than it saves);
 //   * head_dim 64, causal, more than one round of 128-row workgroups and
 //     seq_len <= 2048: 64 rows in two groups, two workgroups resident per CU
-//     (80 KiB of LDS each), whose prologues and epilogues overlap the other's
+//     (56 KiB of LDS each), whose prologues and epilogues overlap the other's
 //     steps ((4,8,2048,64) causal 33.7 -> 28.7 us);
 //   * otherwise 128 rows in two groups (head_dim 64 never gains from 256
 //     rows: 1-4 % slower on every grid measured).

@@ -16,24 +16,33 @@
 namespace fa {
 
 constexpr int kFusedTileKV = 32;  // keys per LDS tile
-constexpr int kFusedStages = 4;   // LDS stages per tensor (K, V) per wave group
+constexpr int kFusedStages = 3;   // LDS stages per tensor (K, V) per wave group
 
 // Pipeline of one group, local step jj (tile jj of the group):
 //   block A  read the V operands of tile jj (LDS -> registers); DMA K tile
 //            jj + kFusedKAhead (its copies spread between the MFMAs);
-//   barrier  wait until only the DMAs of steps jj-1 and jj are in flight and
-//            every LDS read issued so far has completed; workgroup barrier;
+//   barrier  wait until only the last kFusedStepInFlight copy groups are in
+//            flight (block A's K copy) and every LDS read issued so far has
+//            completed; workgroup barrier;
 //   block B  read the K operands of tile jj + 2; DMA V tile jj + kFusedVAhead;
 //            rarely (an exponent-base move), read tile jj's V operands
 //            again at the end of the block.
-// One barrier per step covers both hazards: K_{jj+2} and V_{jj+1} landed
-// before it (read after it), and every stage a later copy overwrites was
-// last read before it or before the previous step's barrier (V_{jj-1}'s
-// stage, the target of block B's copy, was last read in step jj - 1).
-// The prologue copies K_0 .. K_3 and V_0 .. V_2, waits for K_0 and reads
-// its operands, then waits for every prologue copy and reads K_1's operands.
+// One barrier per step covers both hazards: K_{jj+2} (copied in block A of
+// step jj-1) and V_{jj+1} (block B of step jj-1) landed before it and are
+// read after it, and every stage a later copy overwrites was last read
+// before it or before the previous step's barrier (V_{jj-1}'s stage, the
+// target of block B's copy, was last read in step jj - 1). A copy thus has
+// one to one and a half steps to land; with four stages it had two and a
+// half, which measured no faster and costs a deeper prologue.
+// The prologue copies K_0 .. K_{S-1} and V_0 .. V_{S-2}, waits for K_0 and
+// reads its operands, then waits for every prologue copy and reads K_1's
+// operands.
 constexpr int kFusedKAhead = kFusedStages;      // into K_jj's stage (read in step jj - 2)
 constexpr int kFusedVAhead = kFusedStages - 1;  // into V_{jj-1}'s stage (read in step jj - 1)
+// Copy groups (one group = one tile's copies) still in flight at a step's
+// barrier once K_{jj+2} and V_{jj+1} have landed: those issued after V_{jj+1}.
+constexpr int kFusedStepInFlight = 2 * kFusedStages - 5;
+static_assert(kFusedStages >= 3, "K_{jj+2} is read in the step that copies K_{jj+S}: S >= 3");
 
 constexpr int kFusedMaxGroups = 4;  // wave groups (KV streams) per workgroup: 1, 2 or 4
 
@@ -54,11 +63,15 @@ FA_HD inline int fused_group_barriers(int /*g*/, int count) { return 2 + count; 
 // The step walk of one group over its `count` tiles: step(kk, jj) for
 // jj = 0 .. count-1 with kk = jj % kFusedUnroll as a compile-time
 // std::integral_constant: kk % kFusedStages is the LDS stage rotation and
-// kk % 2 the register double buffer of S and P. Each step runs exactly one
-// workgroup barrier.
-constexpr int kFusedUnroll = kFusedStages;
-static_assert(kFusedUnroll % 2 == 0, "the S / P double buffer needs an even unroll");
+// kk % 2 the register double buffer of S and P (kFusedUnroll is the least
+// common multiple of the two). Each step runs exactly one workgroup barrier.
+constexpr int kFusedUnroll = kFusedStages % 2 == 0 ? kFusedStages : 2 * kFusedStages;
+static_assert(kFusedUnroll % 2 == 0 && kFusedUnroll % kFusedStages == 0, "stage rotation and double buffer");
 
+static_assert(kFusedUnroll == 6, "fused_group_walk is written out for six steps per pass");
+
+// Written out step by step: a recursive template form of the same walk
+// made the compiler keep 10-16 more VGPRs live in the kernel.
 template <class Step>
 FA_HD inline void fused_group_walk(int count, Step&& step)
 {
@@ -72,6 +85,10 @@ FA_HD inline void fused_group_walk(int count, Step&& step)
         step(std::integral_constant<int, 2>{}, jj);
         if (++jj >= count) break;
         step(std::integral_constant<int, 3>{}, jj);
+        if (++jj >= count) break;
+        step(std::integral_constant<int, 4>{}, jj);
+        if (++jj >= count) break;
+        step(std::integral_constant<int, 5>{}, jj);
         ++jj;
     }
 }

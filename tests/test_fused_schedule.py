@@ -99,9 +99,10 @@ int main() {
                 // block A: V operands of tile jj; copies of K tile jj+KAhead
                 read(vs, jj % S, jj);
                 dma(ks, (jj + kFusedKAhead) % S, jj + kFusedKAhead, k_consumed);
-                // the step's one barrier: the last three copy groups may
-                // still fly; every LDS read issued so far has completed
-                wait_allow(3);
+                // the step's one barrier: the last kFusedStepInFlight copy
+                // groups may still fly; every LDS read issued so far has
+                // completed
+                wait_allow(kFusedStepInFlight);
                 barrier(); ++barriers;
                 v_consumed = v_pending;
                 k_consumed = k_pending;
@@ -149,7 +150,7 @@ def test_schedule_checker_catches_a_short_pipeline(tmp_path):
         [("for (int x = 0; x < S - 1; ++x) dma(vs, x, x, -1);", "for (int x = 0; x < S; ++x) dma(vs, x, x, -1);"),
          ("dma(vs, (jj + kFusedVAhead) % S, jj + kFusedVAhead, v_consumed);",
           "dma(vs, (jj + kFusedVAhead + 1) % S, jj + kFusedVAhead + 1, v_consumed);")],
-        [("wait_allow(3);", "wait_allow(4);")],
+        [("wait_allow(kFusedStepInFlight);", "wait_allow(kFusedStepInFlight + 1);")],
         [("wait_allow(0);                               // every", "wait_allow(3);                               // every")],
     ]
     for i, subs in enumerate(plants):
