@@ -1422,11 +1422,18 @@ int launch_fused(const void* q, const void* k, const void* v, void* o, int batch
 //     so twice as many workgroups finish sooner; at head_dim 64 with
 //     seq_len >= 1024 split over four KV groups of two waves (every SIMD
 //     keeps two waves: (1,8,2048,64) 14.5 -> 12.9 us), else two groups;
-//   * head_dim 128: 256 rows in one group when even 256-row workgroups give
-//     every CU one (dense), or, causal, for seq_len >= 8192 with at least two
-//     rounds of them: half the L2->LDS copies per score and no merge, 2-7%
-//     faster there; shorter causal sequences lose more to the coarser
-//     diagonal blocks than they gain;
+//   * 256 rows in one group (half the L2->LDS copies per score, no merge):
+//     dense, when even 256-row workgroups give every CU one (head_dim 128:
+//     2-7 % faster; head_dim 64: 0-6 %, e.g. (8,8,1024,64) 22.0 -> 20.6 us);
+//     causal, for seq_len >= 8192 with at least two rounds of them (2-3 %;
+//     shorter sequences with several rounds lose more to the coarser
+//     diagonal blocks than they gain); and causal, when the 128-row grid
+//     needs more than one round but the 256-row grid fits in one, for
+//     seq_len <= 2048 (head_dim 128) or <= 1024 (head_dim 64): one round of
+//     fixed costs instead of two ((16,8,512,128) 25.3 -> 18.4 us,
+//     (8,8,1024,128) 33.6 -> 28.0, (4,8,2048,128) 49.8 -> 48.4,
+//     (16,8,512,64) 14.5 -> 11.8; longer sequences lose to the unsplit
+//     walk of the last block: (2,8,4096,128) 70.5 -> 90.7);
 //   * head_dim 64, causal, exactly one round of 128-row workgroups and
 //     seq_len >= 2048: the list layout (128 rows, four groups of two waves
 //     walking the two half blocks' tiles as one list), which keeps two busy
@@ -1438,8 +1445,7 @@ int launch_fused(const void* q, const void* k, const void* v, void* o, int batch
 //     seq_len <= 2048: 64 rows in two groups, two workgroups resident per CU
 //     (56 KiB of LDS each), whose prologues and epilogues overlap the other's
 //     steps ((4,8,2048,64) causal 33.7 -> 28.7 us);
-//   * otherwise 128 rows in two groups (head_dim 64 never gains from 256
-//     rows: 1-4 % slower on every grid measured).
+//   * otherwise 128 rows in two groups.
 // Dense outputs of the 64- and 128-row two-group configurations are bitwise
 // identical (each wave computes its 32 rows the same way in both).
 struct FusedConfig
@@ -1455,14 +1461,15 @@ FusedConfig auto_config(int batch, int heads, int seq_len, int head_dim, int cau
     const long long cus = device_compute_units();
     const long long blocks128 = bh * ((static_cast<long long>(seq_len) + 127) / 128);
     if (blocks128 < cus) return (head_dim == 64 && seq_len >= 1024) ? FusedConfig{64, 4} : FusedConfig{64, 2};
-    if (head_dim == 128)
+    const long long wide = bh * ((static_cast<long long>(seq_len) + 255) / 256);
+    if (!causal) return wide >= cus ? FusedConfig{256, 1} : FusedConfig{128, 2};
+    if (seq_len >= 8192 && wide >= 2 * cus) return {256, 1};
+    if (blocks128 > cus && wide <= cus && seq_len <= (head_dim == 128 ? 2048 : 1024)) return {256, 1};
+    if (head_dim == 64)
     {
-        const long long wide = bh * ((static_cast<long long>(seq_len) + 255) / 256);
-        if (causal ? (seq_len >= 8192 && wide >= 2 * cus) : wide >= cus) return {256, 1};
-        return {128, 2};
+        if (blocks128 == cus && seq_len >= 2048) return {128, 4};
+        if (blocks128 > cus && seq_len <= 2048) return {64, 2};
     }
-    if (causal && blocks128 == cus && seq_len >= 2048) return {128, 4};
-    if (causal && blocks128 > cus && seq_len <= 2048) return {64, 2};
     return {128, 2};
 }
 

@@ -91,7 +91,8 @@ def test_configuration_rule_without_a_device(fa_lib):
     MI355X's 256): three of the four (2,8,2048,D) metric shapes run 128 rows
     in two groups and (2,8,2048,64) causal, one round of 128-row workgroups,
     the four-group list layout; small head_dim-64 grids take four KV groups;
-    an unsupported head_dim reports no configuration."""
+    256 rows in one group where the rule's three cases apply; an unsupported
+    head_dim reports no configuration."""
     for d in (64, 128):
         for causal in (False, True):
             want = (128, 4) if (d, causal) == (64, True) else (128, 2)
@@ -100,8 +101,19 @@ def test_configuration_rule_without_a_device(fa_lib):
     assert fa_lib.tensorcore_v3_config((1, 4, 8192, 64), True) == (128, 4)
     assert fa_lib.tensorcore_v3_config((1, 8, 2048, 64), True) == (64, 4)
     assert fa_lib.tensorcore_v3_config((1, 8, 512, 64), False) == (64, 2)
-    assert fa_lib.tensorcore_v3_config((4, 8, 8192, 64), False) == (128, 2)
+    assert fa_lib.tensorcore_v3_config((4, 8, 8192, 64), False) == (256, 1)
     assert fa_lib.tensorcore_v3_config((4, 8, 8192, 128), False) == (256, 1)
+    assert fa_lib.tensorcore_v3_config((1, 8, 4096, 128), False) == (128, 2)   # 128 256-row workgroups
+    assert fa_lib.tensorcore_v3_config((4, 8, 2048, 64), True) == (64, 2)
+    # causal, 256 rows: long sequences with two rounds of them, or one round
+    # of them replacing two rounds of 128-row workgroups at short lengths
+    assert fa_lib.tensorcore_v3_config((2, 8, 8192, 64), True) == (256, 1)
+    assert fa_lib.tensorcore_v3_config((1, 8, 8192, 128), True) == (128, 2)
+    assert fa_lib.tensorcore_v3_config((16, 8, 512, 128), True) == (256, 1)
+    assert fa_lib.tensorcore_v3_config((4, 8, 2048, 128), True) == (256, 1)
+    assert fa_lib.tensorcore_v3_config((2, 8, 4096, 128), True) == (128, 2)
+    assert fa_lib.tensorcore_v3_config((12, 8, 1024, 128), True) == (128, 2)  # 1.5 rounds of 256-row
+    assert fa_lib.tensorcore_v3_config((8, 8, 1024, 64), True) == (256, 1)
     assert fa_lib.tensorcore_v3_config((4, 8, 2048, 64), True) == (64, 2)
     assert fa_lib.tensorcore_v3_config((1, 8, 512, 96), False) is None
     assert fa_lib.tensorcore_v3_rows_per_block((1, 8, 512, 96), False) == 0

@@ -194,12 +194,14 @@ def test_v3_and_v3b_agree(fa, oracle_mod):
 def test_v3_picks_the_configuration_by_grid(fa, oracle_mod):
     """The v3 entry's configuration rule: 64 rows per workgroup when the
     128-row grid has fewer workgroups than the device has CUs (four KV groups
-    at head_dim 64 with seq_len >= 1024, else two); at head_dim 128, 256 rows
-    in one group when even 256-row workgroups give every CU one (dense) or,
-    causal, for seq_len >= 8192 with two rounds of them; at head_dim 64,
-    causal, exactly one round and seq_len >= 2048, the four-group list layout
-    (128, 4); at head_dim 64, causal, more than one round and seq_len <= 2048,
-    64 rows in two groups; else 128 rows in two groups. Its output equals the pinned configuration's
+    at head_dim 64 with seq_len >= 1024, else two); 256 rows in one group when
+    even 256-row workgroups give every CU one (dense), or, causal, for
+    seq_len >= 8192 with two rounds of them, or when one round of them
+    replaces more than one of 128-row workgroups at seq_len <= 2048 (head_dim
+    128) or <= 1024 (64); at head_dim 64, causal, exactly one round and
+    seq_len >= 2048, the four-group list layout (128, 4); at head_dim 64,
+    causal, more than one round and seq_len <= 2048, 64 rows in two groups;
+    else 128 rows in two groups. Its output equals the pinned configuration's
     bit for bit on each side of each threshold."""
     cus = fa.query_tensorcore_v3(64)["compute_units"]
     assert cus > 0
@@ -209,13 +211,15 @@ def test_v3_picks_the_configuration_by_grid(fa, oracle_mod):
         ((1, 4, 1024, 128), (False, True), "v3b_mfma"),         # the same at head_dim 128
         ((1, cus // 2, 256, 64), (False, True), "v3_128"),      # `cus` of 128 rows, head_dim 64
         ((1, cus // 2, 256, 128), (False, True), "v3_128"),     # `cus` of 128 rows, `cus`/2 of 256
-        ((1, cus, 256, 128), (False,), "v3_256"),               # `cus` workgroups of 256 rows, dense
-        ((1, cus, 256, 64), (False,), "v3_128"),                # head_dim 64: never 256 rows
+        ((1, cus, 256, 128), (False, True), "v3_256"),          # `cus` workgroups of 256 rows (causal:
+        ((1, cus, 256, 64), (False, True), "v3_256"),           #   one round of them instead of two of 128)
         ((1, cus // 16, 2048, 64), (True,), "v3_128x4"),        # head_dim 64 causal, one round, seq_len 2048
         ((1, cus // 16, 2048, 64), (False,), "v3_128"),         # ... dense
         ((1, cus // 8, 2048, 64), (True,), "v3b_mfma"),         # head_dim 64 causal, 2 rounds, seq_len 2048
         ((1, cus // 16, 4096, 64), (True,), "v3_128"),          # ... and seq_len 4096
         ((1, 2 * cus // 32, 8192, 128), (True,), "v3_256"),     # causal, 2 * `cus` of 256 rows
+        ((1, 2 * cus // 32, 8192, 64), (True,), "v3_256"),      # ... at head_dim 64
+        ((1, cus // 16, 4096, 128), (True,), "v3_128"),         # one round of 256 rows, seq_len 4096
         ((1, 4 * cus // 16, 4096, 128), (True,), "v3_128"),     # causal below 8192 keys
     ]
     for (B, H, N, D), masks, pinned in cases:
