@@ -504,13 +504,21 @@ __device__ __forceinline__ void rescale_o(Frag<D>& f, float alpha)
         for (int r = 0; r < 16; ++r) f.o[db][r] *= alpha;
 }
 
+// Waves per SIMD the kernel is compiled for. A dense head_dim-64 one-group
+// workgroup (256 rows, 8 waves) needs 64 KiB of LDS, so two fit a CU when
+// each wave keeps to 128 VGPRs (four waves per SIMD instead of two). The
+// compiler then spills 5 VGPRs, and grids of several rounds run 5-7 %
+// faster ((4,8,8192,64) 524 -> 489 us, (1,16,16384,64) 1040 -> 970 us),
+// one-round grids within 1 %. The causal kernel stays at two waves per SIMD:
+// with two workgroups per CU it lost 4-41 %.
+template <int D, int kGroups, bool kCausal>
+constexpr int kMinWavesPerSimd = (D == 64 && kGroups == 1 && !kCausal) ? 4 : 1;
+
 template <int D, int kWpg, bool kCausal, int kGroups, bool kList = false>
-__global__ __launch_bounds__(64 * kGroups * kWpg) void fused_attention_kernel(const uint16_t* __restrict__ q,
-                                                                              const uint16_t* __restrict__ k,
-                                                                              const uint16_t* __restrict__ v,
-                                                                              uint16_t* __restrict__ o, int n,
-                                                                              int q_blocks, int total_blocks,
-                                                                              float c_log2, int paired)
+__global__ __launch_bounds__(64 * kGroups * kWpg)
+__attribute__((amdgpu_waves_per_eu(kMinWavesPerSimd<D, kGroups, kCausal>, 8))) void fused_attention_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+    uint16_t* __restrict__ o, int n, int q_blocks, int total_blocks, float c_log2, int paired)
 {
     using C = Cfg<D, kWpg, kGroups, kList>;
     // Group g's K stages, then its V stages, at compile-time offsets of one

@@ -352,8 +352,15 @@ def test_query_reports_resources(fa):
                 assert info["supported"] == 0
                 continue
             assert info["supported"] == 1 and info["rows_per_block"] == rows and info["kv_groups"] == groups
-            assert info["waves_per_block"] * 64 == info["block_size"] and info["local_bytes_per_thread"] == 0
+            assert info["waves_per_block"] * 64 == info["block_size"]
             assert info["agprs_per_thread"] == 0 and info["max_blocks_per_sm"] >= 1
+            if (d, groups) == (64, 1):
+                # the dense head_dim-64 one-group kernel is built for two
+                # workgroups per CU (128 VGPRs, a few spilled)
+                assert info["max_blocks_per_sm"] == 2 and 0 < info["local_bytes_per_thread"] <= 64
+                assert info["registers_per_thread"] <= 128
+            else:
+                assert info["local_bytes_per_thread"] == 0, ("register spill", rows, groups, d)
     for d in (64, 128):
         wide = fa.query_fused(d, 256)
         assert wide["rows_per_block"] == 256 and wide["waves_per_block"] == 8 and wide["block_size"] == 512
@@ -362,7 +369,8 @@ def test_query_reports_resources(fa):
             print(d, info)
             assert info["supported"] == 1
             assert info["registers_per_thread"] > 0
-            assert info["local_bytes_per_thread"] == 0, "register spill"
+            if not (d == 64 and info is wide):
+                assert info["local_bytes_per_thread"] == 0, "register spill"
             assert info["shared_bytes_per_block"] >= 2 * 2 * 32 * d * 2
             assert info["max_blocks_per_sm"] >= 1
             assert info["device_shared_bytes_per_sm"] >= 64 * 1024
