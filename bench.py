@@ -22,7 +22,11 @@ reads up to 10 % slow), then W untimed warmup launches, a synchronisation, and
 K launches bracketed by hipEvents recorded on the launch stream (inside the
 library, fa_time_batch) and by host synchronisation. `value` is the whole-job
 rate over that region, `roofline.achieved` the same FLOPs over the average
-launch duration from the events. Inputs come from the package's seeded
+launch duration from the events. After the timed region a calibration
+kernel measures the dense bf16 matrix rate this box sustains under full MFMA
+load (fa_mfma_peak); `roofline.frac` stays against the published 2.5 PFLOP/s
+and `roofline.frac_of_sustained` divides by that same-run rate, so a change of
+a point or two can be told apart from box-to-box clock spread. Inputs come from the package's seeded
 generator (cuda_fused_attention_amd/inputs.py); only the cpu_baseline leg
 loads the oracle.
 """
@@ -289,6 +293,7 @@ def main():
                     help="kernel in the timed region (v0_unfused: the three-kernel baseline, HBM roofline)")
     ap.add_argument("--no-extras", action="store_true", help="only the timed region (for profiling runs)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-calibration", action="store_true", help="skip the sustained-MFMA-rate calibration")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="also run a plain elementwise copy of this many MiB (rocprof counter calibration)")
     args = ap.parse_args()
@@ -382,6 +387,16 @@ def main():
     avg_launch_ms = event_ms / args.steps
     achieved = flops / (avg_launch_ms * 1e-3) / 1e12
 
+    # Same-run calibration of the sustained matrix rate (after the timed
+    # region: its full-MFMA load lowers the clock): every wave of two per
+    # SIMD issuing back-to-back MFMAs, ~0.3 ms per launch, 20 launches per
+    # run; the best of three runs (the clock under this load moves by up to
+    # ~25 % within a process, so all three are reported).
+    calib, calib_runs = None, []
+    if not args.no_calibration:
+        calib_runs = [fa.mfma_peak(mfma_per_wave=8192, launches=20, stream=stream) for _ in range(3)]
+        calib = max(calib_runs, key=lambda r: r["tflops"])
+
     if args.calib_copy_mib:
         x = torch.ones(args.calib_copy_mib * (1 << 20) // 4, dtype=torch.float32, device="cuda")
         y = torch.empty_like(x)
@@ -434,6 +449,22 @@ def main():
         result["roofline"].update({"bound": "hbm", "achieved": round(gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                                    "frac": round(gbps / PEAK_HBM_GBPS, 5), "algorithmic_bytes_per_launch": v0_bytes,
                                    "bytes_model": "16*B*H*N^2 + 8*B*H*N*D (three kernels per launch)"})
+    if calib is not None and args.kernel != "v0_unfused":
+        # frac stays against the published peak; frac_of_sustained divides by
+        # what this box's matrix pipes sustained in this process.
+        result["roofline"].update({
+            "sustained_peak": round(calib["tflops"], 3),
+            "frac_of_sustained": round(achieved / calib["tflops"], 5),
+            "sustained_clock_ghz": round(calib["clock_ghz"], 4),
+            "sustained_source": f"fa_mfma_peak: one 512-thread workgroup per CU, {calib['mfma_per_wave']} "
+                                "back-to-back v_mfma_f32_32x32x16_bf16 per wave, best of 3 x "
+                                f"{calib['launches']} launches",
+            "sustained_runs": [{"tflops": round(r["tflops"], 1), "clock_ghz": round(r["clock_ghz"], 4)}
+                               for r in calib_runs],
+        })
+        if shapes is not None:
+            for entry in shapes.values():
+                entry["v3_mfma"]["b2b_frac_of_sustained"] = entry["v3_mfma"]["b2b_tflops"] / calib["tflops"]
     result["clock_ramp_launches"] = ramp_launches
     if shapes is not None:
         result["shapes"] = shapes

@@ -97,6 +97,8 @@ _SIGNATURES = {
     "fa_query_fused": (_i, [_i, _i, ctypes.POINTER(TilingInfo)]),
     "fa_launch_attention_fused_groups": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp]),
     "fa_query_fused_groups": (_i, [_i, _i, _i, ctypes.POINTER(TilingInfo)]),
+    "fa_query_fused_config": (_i, [_i, _i, _i, _i, ctypes.POINTER(TilingInfo)]),
+    "fa_query_tensorcore_v3_shape": (_i, [_i, _i, _i, _i, _i, ctypes.POINTER(TilingInfo)]),
     "fa_tensorcore_v3_rows_per_block": (_i, [_i, _i, _i, _i, _i]),
     "fa_tensorcore_v3_config": (_i, [_i, _i, _i, _i, _i, ctypes.POINTER(_i), ctypes.POINTER(_i)]),
     "fa_query_tensorcore_v3": (_i, [_i, ctypes.POINTER(TilingInfo)]),
@@ -109,6 +111,8 @@ _SIGNATURES = {
                               ctypes.POINTER(ctypes.c_float), _vp]),
     "fa_time_batch": (_i, [_i, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i,
                            ctypes.POINTER(ctypes.c_float), _vp]),
+    "fa_mfma_peak_records_bytes": (ctypes.c_size_t, []),
+    "fa_mfma_peak": (_i, [_i, _i, _vp, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double), _vp]),
     "fa_build_info": (ctypes.c_char_p, []),
 }
 
@@ -210,6 +214,23 @@ def query_fused_groups(head_dim: int, rows_per_block: int, kv_groups: int) -> di
     info = TilingInfo()
     _check(lib().fa_query_fused_groups(head_dim, rows_per_block, kv_groups, ctypes.byref(info)),
            "fa_query_fused_groups")
+    return info.as_dict()
+
+
+def query_fused_config(head_dim: int, rows_per_block: int, kv_groups: int, causal: bool) -> dict:
+    """Resources of the kernel (rows_per_block, kv_groups) runs with this mask."""
+    info = TilingInfo()
+    _check(lib().fa_query_fused_config(head_dim, rows_per_block, kv_groups, int(causal), ctypes.byref(info)),
+           "fa_query_fused_config")
+    return info.as_dict()
+
+
+def query_tensorcore_v3_shape(shape, causal: bool) -> dict:
+    """Resources of the kernel the v3 entry launches at this shape and mask."""
+    s = _shape_of(shape)
+    info = TilingInfo()
+    _check(lib().fa_query_tensorcore_v3_shape(s.batch, s.heads, s.seq_len, s.head_dim, int(causal),
+                                              ctypes.byref(info)), "fa_query_tensorcore_v3_shape")
     return info.as_dict()
 
 
@@ -362,6 +383,24 @@ def time_batch(kernel: str, q, k, v, o, workspace, shape, causal: bool, iters: i
     if not _check(st, "fa_time_batch"):
         return None
     return float(total.value)
+
+
+def mfma_peak(mfma_per_wave: int = 8192, launches: int = 5, stream=None) -> dict:
+    """Same-run calibration of the dense bf16 matrix rate the device sustains
+    (fa_mfma_peak): every wave of two per SIMD issuing back-to-back MFMAs.
+    Returns {"tflops", "clock_ghz", "mfma_per_wave", "launches"}."""
+    import torch
+
+    nbytes = lib().fa_mfma_peak_records_bytes()
+    if nbytes == 0:
+        raise FaError(0, "fa_mfma_peak_records_bytes (no device)")
+    records = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    tf, ghz = ctypes.c_double(), ctypes.c_double()
+    st = lib().fa_mfma_peak(mfma_per_wave, launches, _ptr(records), ctypes.byref(tf), ctypes.byref(ghz),
+                            _stream(stream))
+    _check(st, "fa_mfma_peak")
+    return {"tflops": tf.value, "clock_ghz": ghz.value, "mfma_per_wave": mfma_per_wave - mfma_per_wave % 8,
+            "launches": launches}
 
 
 def quantile_type7(values, p: float) -> float:

@@ -16,7 +16,7 @@ LIB_NAME = "libfa_mi355x.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
 ARCH = "gfx950"
 
-SOURCES = ["fa_unfused.hip", "fa_fused.hip", "fa_api.cpp"]
+SOURCES = ["fa_unfused.hip", "fa_fused.hip", "fa_calib.hip", "fa_api.cpp"]
 
 # -packed-fp32-ops: the compiler must not form v_pk_{add,mul,fma}_f32 by
 # itself from float code (those forms have miscomputed on this pool).

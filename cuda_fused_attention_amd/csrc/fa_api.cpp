@@ -145,6 +145,14 @@ FusedTilingInfo query_tensorcore_v3(int head_dim)
     return to_cpp(c);
 }
 
+FusedTilingInfo query_tensorcore_v3(const AttentionShape& s, bool causal)
+{
+    fa_tiling_info c{};
+    if (fa_query_tensorcore_v3_shape(s.batch, s.heads, s.seq_len, s.head_dim, causal ? 1 : 0, &c) != 0)
+        return FusedTilingInfo{};
+    return to_cpp(c);
+}
+
 double tensorcore_v3_hbm_bytes(const AttentionShape& s, bool causal)
 {
     return fa_tensorcore_v3_hbm_bytes(s.batch, s.heads, s.seq_len, s.head_dim, causal ? 1 : 0);

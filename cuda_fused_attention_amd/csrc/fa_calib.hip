@@ -1,0 +1,156 @@
+// Same-run calibration of the device's sustained dense bf16 matrix rate.
+//
+// One 512-thread workgroup per CU (two waves per SIMD, as the fused kernel
+// runs), every wave issuing back-to-back v_mfma_f32_32x32x16_bf16 on four
+// independent accumulators and nothing else in its loop. The rate this
+// reaches is what the matrix pipes sustain at the clock the device holds
+// under full MFMA load, which is below the 2.4 GHz the published 2.5 PFLOP/s
+// assumes; the kernel also stamps the shader clock (s_memtime) against the
+// constant-rate wall clock (s_memrealtime) so the run reports that clock.
+// Neither the reference nor its harness has a counterpart: its numbers are
+// quoted against a fixed published peak only.
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+#include <vector>
+
+#include "fa_common.hpp"
+#include "../../include/fa_mi355x.h"
+
+namespace {
+
+constexpr int kCalibThreads = 512;       // 8 waves: two per SIMD
+constexpr int kCalibMfmaPerIter = 8;     // unrolled MFMAs per loop iteration
+constexpr int kCalibRecordWords = 4;     // uint64 words per workgroup record
+constexpr double kFlopsPerMfma = 2.0 * 32 * 32 * 16;
+
+// Each workgroup writes {shader ticks, wall-clock ticks, accumulator-sum
+// bits, 0} from thread 0; the sum keeps every MFMA live.
+__global__ __launch_bounds__(kCalibThreads) void mfma_peak_kernel(uint64_t* __restrict__ records, int iters)
+{
+    // Operands with hashed mantissas and signs in [-1, -0.5] U [0.5, 1], so
+    // the matrix pipes switch about as much as on attention data (a clock
+    // under power limits depends on it).
+    const uint32_t lane = threadIdx.x & 63;
+    fa::bf16x8 a, b;
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+    {
+        const uint32_t ha = (lane * 8u + e) * 2654435761u;
+        const uint32_t hb = (lane * 8u + e + 512u) * 2246822519u;
+        a[e] = __builtin_bit_cast(__bf16, static_cast<uint16_t>(0x3f00u | ((ha >> 16) & 0x807fu)));
+        b[e] = __builtin_bit_cast(__bf16, static_cast<uint16_t>(0x3f00u | ((hb >> 16) & 0x807fu)));
+    }
+    fa::f32x16 acc0 = {}, acc1 = {}, acc2 = {}, acc3 = {};
+    const uint64_t t0 = __builtin_amdgcn_s_memtime();
+    const uint64_t r0 = __builtin_amdgcn_s_memrealtime();
+    for (int it = 0; it < iters; ++it)
+    {
+        acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc1, 0, 0, 0);
+        acc2 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc2, 0, 0, 0);
+        acc3 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc3, 0, 0, 0);
+        acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc1, 0, 0, 0);
+        acc2 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc2, 0, 0, 0);
+        acc3 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc3, 0, 0, 0);
+    }
+    const uint64_t t1 = __builtin_amdgcn_s_memtime();
+    const uint64_t r1 = __builtin_amdgcn_s_memrealtime();
+    float s = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) s += acc0[e] + acc1[e] + acc2[e] + acc3[e];
+    if (threadIdx.x == 0)
+    {
+        uint64_t* r = records + static_cast<size_t>(blockIdx.x) * kCalibRecordWords;
+        r[0] = t1 - t0;
+        r[1] = r1 - r0;
+        r[2] = __float_as_uint(s);
+        r[3] = 0;
+    }
+}
+
+int device_cus(int* cus)
+{
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    e = hipDeviceGetAttribute(cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess) return e;
+    return *cus > 0 ? hipSuccess : hipErrorInvalidDevice;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t fa_mfma_peak_records_bytes(void)
+{
+    int cus = 0;
+    if (device_cus(&cus) != hipSuccess) return 0;
+    return static_cast<size_t>(cus) * kCalibRecordWords * sizeof(uint64_t);
+}
+
+int fa_mfma_peak(int mfma_per_wave, int launches, void* records, double* tflops, double* clock_ghz, void* stream)
+{
+    if (!records || !tflops || !clock_ghz || mfma_per_wave < kCalibMfmaPerIter || launches < 1)
+        return fa::record_status(hipErrorInvalidValue);
+    *tflops = 0.0;
+    *clock_ghz = 0.0;
+    int cus = 0;
+    int st = device_cus(&cus);
+    if (st != hipSuccess) return fa::record_status(st);
+    int dev = 0, wall_khz = 0;
+    if ((st = hipGetDevice(&dev)) != hipSuccess) return fa::record_status(st);
+    if ((st = hipDeviceGetAttribute(&wall_khz, hipDeviceAttributeWallClockRate, dev)) != hipSuccess)
+        return fa::record_status(st);
+    const int iters = mfma_per_wave / kCalibMfmaPerIter;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    auto* rec = static_cast<uint64_t*>(records);
+
+    hipEvent_t ev[2] = {nullptr, nullptr};
+    auto finish = [&](int status) {
+        for (hipEvent_t e : ev)
+            if (e) (void)hipEventDestroy(e);
+        return fa::record_status(status);
+    };
+    for (hipEvent_t& e : ev)
+        if ((st = hipEventCreate(&e)) != hipSuccess) return finish(st);
+    // One untimed launch (code load, clock ramp), then the timed ones.
+    if ((st = fa::launch_kernel(mfma_peak_kernel, dim3(cus), dim3(kCalibThreads), s, rec, iters)) != hipSuccess)
+        return finish(st);
+    if ((st = hipEventRecord(ev[0], s)) != hipSuccess) return finish(st);
+    for (int l = 0; l < launches; ++l)
+        if ((st = fa::launch_kernel(mfma_peak_kernel, dim3(cus), dim3(kCalibThreads), s, rec, iters)) != hipSuccess)
+            return finish(st);
+    if ((st = hipEventRecord(ev[1], s)) != hipSuccess) return finish(st);
+    if ((st = hipEventSynchronize(ev[1])) != hipSuccess) return finish(st);
+    float ms = 0.0f;
+    if ((st = hipEventElapsedTime(&ms, ev[0], ev[1])) != hipSuccess) return finish(st);
+    if (!(ms > 0.0f)) return finish(hipErrorInvalidValue);
+
+    // Shader clock of the last launch: median over workgroups of shader
+    // ticks per wall-clock second.
+    std::vector<uint64_t> host(static_cast<size_t>(cus) * kCalibRecordWords);
+    if ((st = hipMemcpy(host.data(), rec, host.size() * sizeof(uint64_t), hipMemcpyDeviceToHost)) != hipSuccess)
+        return finish(st);
+    std::vector<double> ghz;
+    for (int w = 0; w < cus; ++w)
+    {
+        const uint64_t ticks = host[static_cast<size_t>(w) * kCalibRecordWords];
+        const uint64_t wall = host[static_cast<size_t>(w) * kCalibRecordWords + 1];
+        if (wall > 0) ghz.push_back(static_cast<double>(ticks) / (static_cast<double>(wall) / (wall_khz * 1e3)) / 1e9);
+    }
+    if (!ghz.empty())
+    {
+        std::nth_element(ghz.begin(), ghz.begin() + ghz.size() / 2, ghz.end());
+        *clock_ghz = ghz[ghz.size() / 2];
+    }
+    const double flops = static_cast<double>(cus) * (kCalibThreads / 64) * iters * kCalibMfmaPerIter * kFlopsPerMfma;
+    *tflops = flops * launches / (ms * 1e-3) / 1e12;
+    return finish(hipSuccess);
+}
+
+}  // extern "C"

@@ -1481,12 +1481,15 @@ FusedConfig auto_config(int batch, int heads, int seq_len, int head_dim, int cau
     return {128, 2};
 }
 
+// Resource report of the kernel a configuration launches for head_dim and
+// the mask (the dense and causal instantiations are separate kernels with
+// their own registers, spills and occupancy).
 template <int kWpg, int kGroups = 2, bool kList = false>
-int query_fused(int head_dim, fa_tiling_info* info)
+int query_fused(int head_dim, fa_tiling_info* info, bool causal = false)
 {
     if (!info) return hipErrorInvalidValue;
     *info = fa_tiling_info{};
-    const void* func = pick_kernel<kWpg, kGroups, kList>(head_dim, false);
+    const void* func = pick_kernel<kWpg, kGroups, kList>(head_dim, causal);
     if (!func) return hipSuccess;  // supported = 0
     info->supported = 1;
     info->block_size = 64 * kGroups * kWpg;
@@ -1527,7 +1530,7 @@ int query_fused(int head_dim, fa_tiling_info* info)
     {
         const fa::KernelResources& r = fa::kFusedKernelResources[x];
         if (r.head_dim == head_dim && r.waves_per_group == kWpg && r.groups == kGroups && r.list == (kList ? 1 : 0) &&
-            r.causal == 0)
+            r.causal == (causal ? 1 : 0))
             info->agprs_per_thread = r.agprs;
     }
     return hipSuccess;
@@ -1617,15 +1620,33 @@ int fa_launch_attention_tensorcore_v3(const void* q, const void* k, const void* 
 
 int fa_query_tensorcore_v3(int head_dim, fa_tiling_info* info) { return fa::record_status(query_fused<4>(head_dim, info)); }
 
+int fa_query_fused_config(int head_dim, int rows_per_block, int kv_groups, int causal, fa_tiling_info* info)
+{
+    const bool c = causal != 0;
+    int status = hipErrorInvalidValue;
+    if (rows_per_block == 128 && kv_groups == 2) status = query_fused<4>(head_dim, info, c);
+    else if (rows_per_block == 64 && kv_groups == 2) status = query_fused<2>(head_dim, info, c);
+    else if (rows_per_block == 256 && kv_groups == 1) status = query_fused<8, 1>(head_dim, info, c);
+    else if (rows_per_block == 64 && kv_groups == 4) status = query_fused<2, 4>(head_dim, info, c);
+    else if (rows_per_block == 128 && kv_groups == 4) status = query_fused<2, 4, true>(head_dim, info, c);
+    return fa::record_status(status);
+}
+
 int fa_query_fused_groups(int head_dim, int rows_per_block, int kv_groups, fa_tiling_info* info)
 {
-    int status = hipErrorInvalidValue;
-    if (rows_per_block == 128 && kv_groups == 2) status = query_fused<4>(head_dim, info);
-    else if (rows_per_block == 64 && kv_groups == 2) status = query_fused<2>(head_dim, info);
-    else if (rows_per_block == 256 && kv_groups == 1) status = query_fused<8, 1>(head_dim, info);
-    else if (rows_per_block == 64 && kv_groups == 4) status = query_fused<2, 4>(head_dim, info);
-    else if (rows_per_block == 128 && kv_groups == 4) status = query_fused<2, 4, true>(head_dim, info);
-    return fa::record_status(status);
+    return fa_query_fused_config(head_dim, rows_per_block, kv_groups, 0, info);
+}
+
+int fa_query_tensorcore_v3_shape(int batch, int heads, int seq_len, int head_dim, int causal, fa_tiling_info* info)
+{
+    if (!info) return fa::record_status(hipErrorInvalidValue);
+    if (head_dim != 64 && head_dim != 128)
+    {
+        *info = fa_tiling_info{};
+        return hipSuccess;  // supported = 0, as fa_query_tensorcore_v3
+    }
+    const FusedConfig c = auto_config(batch, heads, seq_len, head_dim, causal);
+    return fa_query_fused_config(head_dim, c.rows, c.groups, causal, info);
 }
 
 int fa_query_fused(int head_dim, int rows_per_block, fa_tiling_info* info)

@@ -171,6 +171,21 @@ int fa_launch_attention_fused_groups(const void* q, const void* k, const void* v
 int fa_query_fused(int head_dim, int rows_per_block, fa_tiling_info* info);
 int fa_query_fused_groups(int head_dim, int rows_per_block, int kv_groups, fa_tiling_info* info);
 
+/* kernels/v3/v3_tensorcore.cu:752-790 extended to the mask: the reference's
+ * v3 is one kernel per head_dim, while each configuration here has a dense
+ * and a causal instantiation with their own registers, spills and occupancy
+ * (fa_query_fused and fa_query_fused_groups describe the dense one).
+ * fa_query_fused_config reports the kernel fa_launch_attention_fused_groups
+ * runs for (rows_per_block, kv_groups) with this mask;
+ * fa_query_tensorcore_v3_shape reports the kernel
+ * fa_launch_attention_tensorcore_v3 launches at this shape and mask on the
+ * current device (its configuration as fa_tensorcore_v3_config names it).
+ * An unsupported head_dim gives supported = 0 and status 0, as
+ * fa_query_tensorcore_v3. */
+int fa_query_fused_config(int head_dim, int rows_per_block, int kv_groups, int causal, fa_tiling_info* info);
+int fa_query_tensorcore_v3_shape(int batch, int heads, int seq_len, int head_dim, int causal,
+                                 fa_tiling_info* info);
+
 /* No counterpart in the reference (whose v3 has one configuration): the
  * workgroup configuration fa_launch_attention_tensorcore_v3 runs at this
  * shape on the current device, as (query rows per workgroup, KV wave groups):
@@ -222,6 +237,23 @@ int fa_time_launches(int which, const void* q, const void* k, const void* v, voi
 int fa_time_batch(int which, const void* q, const void* k, const void* v, void* o,
                   float* workspace, int batch, int heads, int seq_len, int head_dim,
                   int causal, int iters, float* total_ms, void* stream);
+
+/* No counterpart in the reference (its numbers are quoted against a fixed
+ * published peak only): a same-run calibration of the dense bf16 matrix
+ * rate the device sustains. One untimed launch, then `launches` timed
+ * launches (one hipEvent pair on `stream`) of a kernel with one 512-thread
+ * workgroup per CU in which every wave (two per SIMD) issues
+ * `mfma_per_wave` (>= 8; rounded down to a multiple of 8) back-to-back
+ * v_mfma_f32_32x32x16_bf16 on four independent accumulators. `records` is a
+ * device buffer of fa_mfma_peak_records_bytes() bytes (the kernel's per-
+ * workgroup clock stamps). Synchronises `stream`. *tflops: the rate over the
+ * timed launches; *clock_ghz: the median shader clock of the last launch
+ * (s_memtime ticks over s_memrealtime wall time). For bench.py's
+ * roofline.sustained_peak: the published 2.5 PFLOP/s assumes 2.4 GHz, which
+ * the device does not hold under full MFMA load. */
+size_t fa_mfma_peak_records_bytes(void);
+int fa_mfma_peak(int mfma_per_wave, int launches, void* records, double* tflops, double* clock_ghz,
+                 void* stream);
 
 /* Library identification: "gfx950" and the build's kernel configuration. */
 const char* fa_build_info(void);

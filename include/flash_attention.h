@@ -117,6 +117,11 @@ void launch_attention_tensorcore_v3(const __hip_bfloat16* q, const __hip_bfloat1
 
 FusedTilingInfo query_tensorcore_v3(int head_dim);
 
+// Not in the reference (whose v3 is one kernel per head_dim): the resources
+// of the kernel launch_attention_tensorcore_v3 runs at this shape and mask
+// (the workgroup configuration it picks, dense or causal instantiation).
+FusedTilingInfo query_tensorcore_v3(const AttentionShape& shape, bool causal);
+
 double tensorcore_v3_hbm_bytes(const AttentionShape& shape, bool causal);
 
 // v3b slot: the same MFMA kernel with 64 query rows per workgroup.

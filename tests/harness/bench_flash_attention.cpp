@@ -479,6 +479,29 @@ int main(int argc, char** argv)
                         info.block_size, info.registers_per_thread, info.agprs_per_thread, info.shared_bytes_per_block,
                         info.max_blocks_per_sm);
         }
+    // The kernel v3 itself launches at BASELINE's four metric shapes: its
+    // configuration and the instantiation for the mask (dense and causal
+    // builds of a configuration differ in registers, spills and occupancy).
+    std::printf("\nv3 at the metric shapes (fa_tensorcore_v3_config, query_tensorcore_v3(shape, causal)):\n"
+                "  %-18s %6s %8s %9s %6s %6s %6s %12s %10s\n",
+                "shape", "mask", "q_rows", "kv_groups", "VGPRs", "AGPRs", "local", "shared/block", "blocks/CU");
+    for (int d : {64, 128})
+        for (bool causal : {false, true})
+        {
+            const fa::AttentionShape s{2, 8, 2048, d};
+            int rows = 0, groups = 0;
+            if (fa_tensorcore_v3_config(s.batch, s.heads, s.seq_len, d, causal ? 1 : 0, &rows, &groups) != 0) return 2;
+            fa_tiling_info info{};
+            if (fa_query_tensorcore_v3_shape(s.batch, s.heads, s.seq_len, d, causal ? 1 : 0, &info) != 0) return 2;
+            const fa::FusedTilingInfo cpp = fa::query_tensorcore_v3(s, causal);
+            if (cpp.registers_per_thread != info.registers_per_thread || cpp.rows_per_block != info.rows_per_block)
+                return 2;
+            char name[32];
+            std::snprintf(name, sizeof(name), "(2,8,2048,%d)", d);
+            std::printf("  %-18s %6s %8d %9d %6d %6d %5dB %11dB %10d\n", name, causal ? "causal" : "dense", rows,
+                        groups, info.registers_per_thread, info.agprs_per_thread, info.local_bytes_per_thread,
+                        info.shared_bytes_per_block, info.max_blocks_per_sm);
+        }
     std::printf("\n");
 
     const std::vector<Entry> table = entries();

@@ -347,20 +347,43 @@ def test_error_paths_leave_output_untouched(fa, oracle_mod):
 def test_query_reports_resources(fa):
     for rows, groups in fa.FUSED_CONFIGS.values():
         for d in (64, 128):
-            info = fa.query_fused_groups(d, rows, groups)
-            if groups == 4 and d == 128:
-                assert info["supported"] == 0
-                continue
-            assert info["supported"] == 1 and info["rows_per_block"] == rows and info["kv_groups"] == groups
-            assert info["waves_per_block"] * 64 == info["block_size"]
-            assert info["agprs_per_thread"] == 0 and info["max_blocks_per_sm"] >= 1
-            if (d, groups) == (64, 1):
-                # the dense head_dim-64 one-group kernel is built for two
-                # workgroups per CU (128 VGPRs, a few spilled)
-                assert info["max_blocks_per_sm"] == 2 and 0 < info["local_bytes_per_thread"] <= 64
-                assert info["registers_per_thread"] <= 128
-            else:
-                assert info["local_bytes_per_thread"] == 0, ("register spill", rows, groups, d)
+            assert fa.query_fused_groups(d, rows, groups) == fa.query_fused_config(d, rows, groups, False)
+            for causal in (False, True):
+                info = fa.query_fused_config(d, rows, groups, causal)
+                if groups == 4 and d == 128:
+                    assert info["supported"] == 0
+                    continue
+                assert info["supported"] == 1 and info["rows_per_block"] == rows and info["kv_groups"] == groups
+                assert info["waves_per_block"] * 64 == info["block_size"]
+                assert info["agprs_per_thread"] == 0 and info["max_blocks_per_sm"] >= 1
+                if (d, groups, causal) == (64, 1, False):
+                    # the dense head_dim-64 one-group kernel is built for two
+                    # workgroups per CU (at most 128 VGPRs); the compiler may
+                    # spill a few values, which lie outside the step loop
+                    # (test_capi_host.py::test_no_spill_traffic_in_step_loops)
+                    assert info["max_blocks_per_sm"] == 2 and info["local_bytes_per_thread"] <= 64
+                    assert info["registers_per_thread"] <= 128
+                else:
+                    assert info["local_bytes_per_thread"] == 0, ("register spill", rows, groups, d, causal)
+
+
+def test_query_describes_the_launched_kernel(fa):
+    """query_tensorcore_v3(shape, causal) reports the instantiation v3 runs:
+    at the four metric shapes, the configuration fa_tensorcore_v3_config
+    names with the mask's own build (c2 causal: the (128, 4) list kernel)."""
+    seen = {}
+    for d in (64, 128):
+        for causal in (False, True):
+            shape = fa.AttentionShape(2, 8, 2048, d)
+            rows, groups = fa.tensorcore_v3_config(shape, causal)
+            info = fa.query_tensorcore_v3_shape(shape, causal)
+            print((2, 8, 2048, d), "causal" if causal else "dense", (rows, groups), info)
+            assert info == fa.query_fused_config(d, rows, groups, causal)
+            assert info["rows_per_block"] == rows and info["kv_groups"] == groups
+            assert info["local_bytes_per_thread"] == 0 and info["agprs_per_thread"] == 0
+            seen[(d, causal)] = (rows, groups)
+    assert seen[(64, True)] == (128, 4)
+    assert fa.query_tensorcore_v3_shape(fa.AttentionShape(2, 8, 2048, 96), False)["supported"] == 0
     for d in (64, 128):
         wide = fa.query_fused(d, 256)
         assert wide["rows_per_block"] == 256 and wide["waves_per_block"] == 8 and wide["block_size"] == 512
