@@ -1536,22 +1536,53 @@ int query_fused(int head_dim, fa_tiling_info* info, bool causal = false)
     return hipSuccess;
 }
 
-// kernels/v3/v3_tensorcore.cu:795-818 accounting for this tiling: Q read and
-// O written once, K and V tiles counted once per query block that loads them.
-double blocked_hbm_bytes(int batch, int heads, int seq_len, int head_dim, int causal, int rows_per_block)
+// kernels/v3/v3_tensorcore.cu:795-818 accounting for the layout a
+// configuration launches: Q read and O written once, and every K/V tile
+// counted once per workgroup that loads it, i.e. the tiles its wave groups
+// walk. Contiguous blocks (dense, and causal grids of several rounds) walk
+// the tiles up to the block's last row, as in the reference's model. Causal
+// grids of one round pair half blocks p and last - p: a two-group
+// workgroup walks the tiles up to the later half block's last row, and the
+// list layout (128 rows, four groups) walks each half block's tiles in turn,
+// so the tiles both need are loaded twice.
+double blocked_hbm_bytes(int batch, int heads, int seq_len, int head_dim, int causal, int rows_per_block,
+                         int kv_groups = 0)
 {
     if (batch <= 0 || heads <= 0 || seq_len <= 0 || head_dim <= 0) return 0.0;
     const double element = 2.0;
     const double slabs = static_cast<double>(batch) * heads;
-    const int row_blocks = (seq_len + rows_per_block - 1) / rows_per_block;
-    double bytes = 2.0 * slabs * seq_len * static_cast<double>(head_dim) * element;
-    double kv_tiles = 0.0;
-    for (int block = 0; block < row_blocks; ++block)
+    const int n = seq_len;
+    const bool list = rows_per_block == 128 && kv_groups == 4;
+    const int row_blocks = (n + rows_per_block - 1) / rows_per_block;
+    const bool paired = causal && (kv_groups == 2 || list) &&
+                        slabs * row_blocks <= static_cast<double>(device_compute_units());
+    auto tiles_to = [&](int last_row) { return static_cast<double>(min(last_row, n - 1) / kTileKV + 1); };
+    double kv_tiles = 0.0;  // per slab
+    if (!paired)
     {
-        const int q_max = block * rows_per_block + rows_per_block - 1;
-        const int key_limit = causal ? (q_max < seq_len - 1 ? q_max : seq_len - 1) : seq_len - 1;
-        kv_tiles += static_cast<double>(key_limit / kTileKV + 1);
+        for (int block = 0; block < row_blocks; ++block)
+        {
+            const int r0 = block * rows_per_block;
+            const int last = causal ? r0 + rows_per_block - 1 : n - 1;
+            if (!list) kv_tiles += tiles_to(last);
+            else  // the block's two halves, each walked whole (a half past n walks nothing)
+                kv_tiles += tiles_to(causal ? r0 + rows_per_block / 2 - 1 : last) +
+                            (r0 + rows_per_block / 2 < n ? tiles_to(last) : 0.0);
+        }
     }
+    else
+    {
+        const int half = rows_per_block / 2;
+        const int n_half = (n + half - 1) / half;
+        const int pairs = (n_half + 1) / 2;
+        for (int pa = 0; pa < pairs; ++pa)
+        {
+            const int pb = n_half - 1 - pa;  // == pa: the middle half block of an odd count, unpaired
+            if (list) kv_tiles += tiles_to(pa * half + half - 1) + (pb > pa ? tiles_to(pb * half + half - 1) : 0.0);
+            else kv_tiles += tiles_to((pb > pa ? pb : pa) * half + half - 1);
+        }
+    }
+    double bytes = 2.0 * slabs * n * static_cast<double>(head_dim) * element;
     bytes += 2.0 * slabs * kv_tiles * kTileKV * head_dim * element;
     return bytes;
 }
@@ -1658,8 +1689,8 @@ int fa_query_fused(int head_dim, int rows_per_block, fa_tiling_info* info)
 // or 256 query rows per workgroup; 32-key tiles).
 double fa_tensorcore_v3_hbm_bytes(int batch, int heads, int seq_len, int head_dim, int causal)
 {
-    return blocked_hbm_bytes(batch, heads, seq_len, head_dim, causal,
-                             auto_config(batch, heads, seq_len, head_dim, causal).rows);
+    const FusedConfig c = auto_config(batch, heads, seq_len, head_dim, causal);
+    return blocked_hbm_bytes(batch, heads, seq_len, head_dim, causal, c.rows, c.groups);
 }
 
 int fa_tensorcore_v3b_supported(int head_dim) { return head_dim == 64 || head_dim == 128; }
@@ -1674,7 +1705,7 @@ int fa_query_tensorcore_v3b(int head_dim, fa_tiling_info* info) { return fa::rec
 
 double fa_tensorcore_v3b_hbm_bytes(int batch, int heads, int seq_len, int head_dim, int causal)
 {
-    return blocked_hbm_bytes(batch, heads, seq_len, head_dim, causal, 64);
+    return blocked_hbm_bytes(batch, heads, seq_len, head_dim, causal, 64, 2);
 }
 
 }  // extern "C"

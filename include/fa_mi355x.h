@@ -203,10 +203,15 @@ int fa_tensorcore_v3_rows_per_block(int batch, int heads, int seq_len, int head_
 int fa_query_tensorcore_v3(int head_dim, fa_tiling_info* info);
 
 /* include/flash_attention.h:96, kernels/v3/v3_tensorcore.cu:795-818 — the
- * algorithmic HBM model of the fused kernel in the configuration the v3
- * entry runs at this shape: Q read and O written once, K/V tiles counted
- * once per query block that loads them (an upper bound; L2 reuse brings the
- * measured figure to Q+K+V+O once). */
+ * algorithmic HBM model of the fused kernel in the configuration and layout
+ * the v3 entry runs at this shape: Q read and O written once, every K/V
+ * tile counted once per workgroup that walks it. Contiguous row blocks walk
+ * the tiles up to their last key (the reference's accounting); causal grids
+ * of one round pair half blocks p and last - p, so a two-group workgroup
+ * walks up to its later half block's last key and the list layout walks
+ * both half blocks' tiles, the shared ones twice (at (2,8,2048,64) causal
+ * 1056 tiles per slab against 544 for contiguous blocks). An upper bound on
+ * HBM traffic: L2 reuse brings the measured figure to Q+K+V+O once. */
 double fa_tensorcore_v3_hbm_bytes(int batch, int heads, int seq_len, int head_dim, int causal);
 
 /* include/flash_attention.h:101-107 — the reference's v3b occupancy variant.
@@ -223,7 +228,8 @@ double fa_tensorcore_v3b_hbm_bytes(int batch, int heads, int seq_len, int head_d
  * `warmup` untimed launches of kernel `which` (0 = unfused, 1 = v3 fused,
  * 2 = v3b fused, 3 = fused with 128 rows per workgroup whatever the shape,
  * 4 = fused with 256 rows per workgroup, 5 = fused with 64 rows and four
- * KV groups),
+ * KV groups, 6 = fused with 128 rows and four KV groups: the list layout,
+ * head_dim 64),
  * synchronise, then `iters` launches each bracketed by
  * hipEventRecord on `stream`; elapsed milliseconds go to samples_ms[iters].
  * Returns FA_ERROR_UNSUPPORTED for an unsupported head_dim and

@@ -183,6 +183,13 @@ def make_inputs(batch, heads, seq_len, head_dim, family: str = "uniform", seeds=
     Families: uniform (BASELINE), normal_mt19937 (the reference's inputs),
     stress (Q,K ~ N(0, 3^2), V uniform), zeros (Q=K=0, V uniform), ones,
     ramp (V[i] = (i mod D) - D/2, Q/K uniform), scaled (Q,K uniform x4).
+    The reference's own five boundary families
+    (kernels/ablation/experiments.cu:283-289), all on its normal(0,1)
+    mt19937 inputs with seeds 11/22/33: ref_normal (that base), ref_zeros
+    (Q=K=V=0), ones (shared with the list above), ref_ramp (V[i] =
+    (i mod D) - D/2 over the normal Q and K) and ref_scaled (the normal Q
+    and K times 4, rounded to bf16 again: exact, a power of two; logits of
+    standard deviation about 16 at the 1/sqrt(D) scale).
     """
     shape = (batch, heads, seq_len, head_dim)
     s = dict(SEEDS)
@@ -205,6 +212,19 @@ def make_inputs(batch, heads, seq_len, head_dim, family: str = "uniform", seeds=
         idx = np.arange(batch * heads * seq_len * head_dim, dtype=np.int64).reshape(shape)
         ramp = (idx % head_dim - head_dim // 2).astype(np.float32)
         return fill_uniform(shape, s["q"]), fill_uniform(shape, s["k"]), bf16_bits(ramp)
+    if family in ("ref_normal", "ref_ramp", "ref_scaled"):
+        q, k, v = (fill_normal_mt19937(shape, s["q"]), fill_normal_mt19937(shape, s["k"]),
+                   fill_normal_mt19937(shape, s["v"]))
+        if family == "ref_ramp":
+            idx = np.arange(batch * heads * seq_len * head_dim, dtype=np.int64).reshape(shape)
+            v = bf16_bits((idx % head_dim - head_dim // 2).astype(np.float32))
+        elif family == "ref_scaled":
+            q = bf16_bits(bf16_to_f32(q) * 4.0)
+            k = bf16_bits(bf16_to_f32(k) * 4.0)
+        return q, k, v
+    if family == "ref_zeros":
+        z = np.zeros(shape, dtype=np.uint16)
+        return z, z.copy(), z.copy()
     if family == "scaled":
         q = bf16_bits(bf16_to_f32(fill_uniform(shape, s["q"])) * 4.0)
         k = bf16_bits(bf16_to_f32(fill_uniform(shape, s["k"])) * 4.0)

@@ -15,12 +15,16 @@
 //     BASELINE's gate (abs_gate <= 1: |O - O_ref| <= 2^-7 max|O_ref row|).
 // Test infrastructure: the FP64 oracle (oracle/liboracle.so) is the checker.
 //
-// Usage: bench_flash_attention [--quick | --accuracy-only] [output_directory]
+// Usage: bench_flash_attention [--quick | --accuracy-only] [--workspace-cap=BYTES] [output_directory]
 //        bench_flash_attention --v0-profile [--check] [output_directory]
 //        bench_flash_attention --v0-profile B H N D causal [samples [warmup]] [output_directory]
 //        bench_flash_attention --v0-profile --profiler B H N D causal [iterations]
 //   --quick          B = 1, N in {512, 2048} only (eight grid cases).
 //   --accuracy-only  the accuracy suite alone (the ctest).
+//   --workspace-cap=BYTES  treat a grid case's v0 workspace above BYTES as
+//                    an allocation failure (the reference's out-of-memory
+//                    path: v0 SKIP "workspace_allocation_failed", the run
+//                    goes on).
 //   --v0-profile     the v0 stage profile (benchmarks/profile_attention_v0.cu):
 //                    the instrumented launch must equal the plain one bit for
 //                    bit (with events, on a non-default stream, and without
@@ -365,13 +369,62 @@ bool v0_profile_launches(const fa::AttentionShape& s, bool causal, int iteration
 
 }  // namespace
 
+namespace {
+
+// The v0 workspace of one grid case (benchmarks/bench_flash_attention.cu:614-629):
+// an allocation that fails for lack of device memory is not an error. It
+// prints a note, clears HIP's error state, and returns nullptr, so v0 is
+// skipped for that case while the run goes on; any other failure stops the
+// run. A request above `cap` bytes (--workspace-cap) takes the same path
+// without asking the device, so it can be exercised on purpose.
+void* allocate_workspace(size_t bytes, size_t cap, const fa::AttentionShape& s)
+{
+    void* ws = nullptr;
+    const hipError_t status = bytes > cap ? hipErrorOutOfMemory : hipMalloc(&ws, bytes);
+    if (status == hipErrorOutOfMemory)
+    {
+        if (bytes <= cap)
+        {
+            const hipError_t last = hipGetLastError();
+            if (last != hipErrorOutOfMemory) HIP_OK(last);
+        }
+        std::fprintf(stderr, "V0 workspace allocation failed: B=%d H=%d N=%d D=%d, %.1f MiB.\n", s.batch, s.heads,
+                     s.seq_len, s.head_dim, bytes / (1024.0 * 1024.0));
+        return nullptr;
+    }
+    HIP_OK(status);
+    return ws;
+}
+
+// Why a table entry does not run for a grid case, or nullptr when it runs
+// (benchmarks/bench_flash_attention.cu:655-656).
+const char* skip_reason(bool supported, bool needs_workspace, bool have_workspace)
+{
+    if (!supported) return "unsupported";
+    if (needs_workspace && !have_workspace) return "workspace_allocation_failed";
+    return nullptr;
+}
+
+// The summary.csv row of a skipped entry: status = the reason, no timing
+// columns, the traffic model and the workspace size (:657-666).
+void write_skip_row(std::ostream& csv, const char* name, const fa::AttentionShape& s, bool causal, const char* reason,
+                    double model_gb, size_t workspace_bytes)
+{
+    key(csv, name, s, causal);
+    csv << ',' << reason << ",0,0,,,,,,,," << model_gb << ',' << workspace_bytes << ",,\n";
+}
+
+}  // namespace
+
+#ifndef FA_HARNESS_NO_MAIN
 int main(int argc, char** argv)
 {
     bool quick = false, accuracy_only = false, v0_profile = false, check_only = false, profiler = false;
+    size_t workspace_cap = SIZE_MAX;  // --workspace-cap=BYTES
     std::filesystem::path out_dir = "results/raw/flash_attention";
     std::vector<int> numbers;  // --v0-profile shape: B H N D causal [samples [warmup] | iterations]
     auto usage = [&](int status) {
-        std::printf("usage: %s [--quick | --accuracy-only] [output_directory]\n"
+        std::printf("usage: %s [--quick | --accuracy-only] [--workspace-cap=BYTES] [output_directory]\n"
                     "       %s --v0-profile [--check] [output_directory]\n"
                     "       %s --v0-profile B H N D causal [samples [warmup]] [output_directory]\n"
                     "       %s --v0-profile --profiler B H N D causal [iterations]\n",
@@ -388,6 +441,14 @@ int main(int argc, char** argv)
         else if (arg == "--v0-profile") v0_profile = true;
         else if (arg == "--check") check_only = true;
         else if (arg == "--profiler") profiler = true;
+        else if (arg.rfind("--workspace-cap=", 0) == 0)
+        {
+            const std::string num = arg.substr(16);
+            char* cap_end = nullptr;
+            const unsigned long long cap = std::strtoull(num.c_str(), &cap_end, 10);
+            if (num.empty() || *cap_end != '\0') return usage(2);
+            workspace_cap = static_cast<size_t>(cap);
+        }
         else if (arg == "--help" || arg == "-h") return usage(0);
         else if (arg.rfind("--", 0) == 0) return usage(2);
         else if (v0_profile && !arg.empty() && *end == '\0' && value >= 0 && value <= 1 << 30)
@@ -580,9 +641,8 @@ int main(int argc, char** argv)
                     fa_oracle_fill_uniform(host.data(), static_cast<int64_t>(n), grid_seed(33, s));
                     HIP_OK(hipMemcpy(v.ptr, host.data(), n * 2, hipMemcpyHostToDevice));
                     const size_t ws_bytes = fa::unfused_workspace_bytes(s);
-                    void* ws = nullptr;
-                    const bool have_ws = hipMalloc(&ws, ws_bytes) == hipSuccess;
-                    if (!have_ws) (void)hipGetLastError();
+                    void* ws = allocate_workspace(ws_bytes, workspace_cap, s);
+                    const bool have_ws = ws != nullptr;
                     const Problem p{q.bf16(), k.bf16(), v.bf16(), o.bf16(), static_cast<float*>(ws), s, causal};
                     // 4*B*H*N^2*D, halved for causal (BASELINE's convention)
                     const double flops = 4.0 * b * s.heads * static_cast<double>(nlen) * nlen * d * (causal ? 0.5 : 1.0);
@@ -596,14 +656,12 @@ int main(int argc, char** argv)
                     for (const Entry& e : table)
                     {
                         const double gb = e.hbm_bytes(s, causal) / 1e9;
-                        const char* skip = !e.supported(d) ? "unsupported"
-                                           : (e.needs_workspace && !have_ws ? "workspace_allocation_failed" : nullptr);
+                        const char* skip = skip_reason(e.supported(d), e.needs_workspace, have_ws);
                         if (skip)
                         {
                             ++skipped;
                             std::printf("  %-16s SKIP (%s)\n", e.name, skip);
-                            key(summary_csv, e.name, s, causal);
-                            summary_csv << ',' << skip << ",0,0,,,,,,,," << gb << ',' << ws_bytes << ",,\n";
+                            write_skip_row(summary_csv, e.name, s, causal, skip, gb, ws_bytes);
                             continue;
                         }
                         HIP_OK(hipMemset(o.ptr, 0xff, n * 2));
@@ -643,3 +701,4 @@ int main(int argc, char** argv)
                 out_dir.string().c_str());
     return all_ok ? 0 : 1;
 }
+#endif  // FA_HARNESS_NO_MAIN

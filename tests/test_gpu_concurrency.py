@@ -45,7 +45,9 @@ def test_two_threads_two_streams(fa, oracle_mod):
             errors.append(repr(exc))
 
     say("concurrency threads")
-    threads = [threading.Thread(target=worker, args=([0, 2],)), threading.Thread(target=worker, args=([1, 3],))]
+    # every case runs in a thread, the two head_dim-64 four-group
+    # configurations (64, 4) and the (128, 4) list layout included
+    threads = [threading.Thread(target=worker, args=([0, 2, 4],)), threading.Thread(target=worker, args=([1, 3, 5],))]
     for t in threads:
         t.start()
     for t in threads:

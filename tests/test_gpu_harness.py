@@ -87,3 +87,30 @@ def test_v0_profile_modes(tmp_path):
     assert "3 iteration(s), output finite" in run.stdout
     bad = subprocess.run([BINARY, "--v0-profile", "--profiler"], capture_output=True, text=True, timeout=60)
     assert bad.returncode == 2
+
+
+def test_grid_goes_on_when_v0_workspace_fails(tmp_path):
+    """The reference's out-of-memory path (benchmarks/bench_flash_attention.cu:
+    614-629,655-667), forced with --workspace-cap=0: every grid case's v0
+    allocation "fails", v0 is skipped with status workspace_allocation_failed
+    and the run goes on, timing the fused kernels of every case (without a
+    speed-up, since there is no baseline)."""
+    if not os.path.exists(BINARY):
+        pytest.fail(f"{BINARY} is missing: run __graft_entry__.build()")
+    print("harness --quick --workspace-cap=0", flush=True)
+    run = subprocess.run([BINARY, "--quick", "--workspace-cap=0", str(tmp_path)], capture_output=True, text=True,
+                         timeout=300)
+    assert run.returncode == 0, run.stdout[-3000:] + run.stderr[-2000:]
+    assert run.stderr.count("V0 workspace allocation failed") == 8
+    fields, summ = rows(tmp_path / "summary.csv")
+    assert fields == SUMMARY and len(summ) == 8 * 6
+    for r in summ:
+        if r["kernel"] == "v0_unfused":
+            assert r["status"] == "workspace_allocation_failed" and r["median_ms"] == "", r
+            assert int(r["v0_workspace_bytes"]) == 8 * int(r["seq_len"]) ** 2 * 4
+        elif r["kernel"] in ("v3_tensorcore", "v3b_tensorcore"):
+            assert r["status"] == "ok" and float(r["median_ms"]) > 0 and r["speedup_vs_v0"] == "", r
+        else:
+            assert r["status"] == "unsupported"
+    assert "48 kernel/shape runs skipped" not in run.stdout  # the fused rows did run
+    assert "32 kernel/shape runs skipped" in run.stdout       # 8 x (v0 + v1 + v2a + v2b)

@@ -257,7 +257,39 @@ def test_one_hot_logit_selects_v_row(oracle_mod):
     np.testing.assert_allclose(outc[0, 0, winner:], np.broadcast_to(oracle_mod.bf16_to_f32(v[0, 0, winner]), (N - winner, D)), rtol=1e-15)
 
 
-@pytest.mark.parametrize("family", ["uniform", "scaled", "ramp", "stress", "normal_mt19937"])
+def test_reference_boundary_families(oracle_mod):
+    """The reference's five boundary families (kernels/ablation/experiments.cu:
+    283-289) as the oracle builds them: the normal(0,1) mt19937 base with
+    seeds 11/22/33, Q=K=V=0 (every output exactly 0: uniform weights over a
+    zero V), all ones (every output 1), the ramp V (integers -D/2 .. D/2-1
+    along the head dim) over the same normal Q and K, and the normal Q and K
+    times 4 (exact in bf16; logits of standard deviation about 16)."""
+    shape = (1, 2, 129, 64)
+    base = oracle_mod.make_inputs(*shape, "normal_mt19937")
+    normal = oracle_mod.make_inputs(*shape, "ref_normal")
+    for a, b in zip(base, normal):
+        assert np.array_equal(a, b)
+    q, k, v = oracle_mod.make_inputs(*shape, "ref_zeros")
+    assert not q.any() and not k.any() and not v.any()
+    for causal in (False, True):
+        assert np.array_equal(oracle_mod.attention(q, k, v, causal), np.zeros(shape))
+    q, k, v = oracle_mod.make_inputs(*shape, "ref_ramp")
+    assert np.array_equal(q, base[0]) and np.array_equal(k, base[1])
+    vf = oracle_mod.bf16_to_f32(v)
+    assert np.array_equal(vf[0, 1, 7], np.arange(64, dtype=np.float32) - 32)
+    q, k, v = oracle_mod.make_inputs(*shape, "ref_scaled")
+    assert np.array_equal(oracle_mod.bf16_to_f32(q), 4 * oracle_mod.bf16_to_f32(base[0]))
+    assert np.array_equal(oracle_mod.bf16_to_f32(k), 4 * oracle_mod.bf16_to_f32(base[1]))
+    assert np.array_equal(v, base[2])
+    logits = np.einsum("hnd,hmd->hnm", oracle_mod.bf16_to_f32(q)[0].astype(np.float64),
+                       oracle_mod.bf16_to_f32(k)[0].astype(np.float64)) / np.sqrt(64.0)
+    assert 13.0 < logits.std() < 19.0
+    for causal in (False, True):
+        assert np.all(np.isfinite(oracle_mod.attention(q, k, v, causal)))
+
+
+@pytest.mark.parametrize("family", ["uniform", "scaled", "ramp", "stress", "normal_mt19937", "ref_ramp",
+                                    "ref_scaled"])
 @pytest.mark.parametrize("causal", [False, True])
 def test_brute_force_long_double(oracle_mod, family, causal):
     for (B, H, N, D) in [(1, 2, 9, 64), (2, 1, 33, 128), (1, 1, 64, 64)]:
