@@ -112,7 +112,7 @@ _SIGNATURES = {
     "fa_time_batch": (_i, [_i, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i,
                            ctypes.POINTER(ctypes.c_float), _vp]),
     "fa_mfma_peak_records_bytes": (ctypes.c_size_t, []),
-    "fa_mfma_peak": (_i, [_i, _i, _vp, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double), _vp]),
+    "fa_mfma_peak": (_i, [_vp, _i, _i, _vp, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double), _vp]),
     "fa_build_info": (ctypes.c_char_p, []),
 }
 
@@ -385,19 +385,26 @@ def time_batch(kernel: str, q, k, v, o, workspace, shape, causal: bool, iters: i
     return float(total.value)
 
 
-def mfma_peak(mfma_per_wave: int = 8192, launches: int = 5, stream=None) -> dict:
+def mfma_peak(mfma_per_wave: int = 8192, launches: int = 5, operands=None, stream=None) -> dict:
     """Same-run calibration of the dense bf16 matrix rate the device sustains
     (fa_mfma_peak): every wave of two per SIMD issuing back-to-back MFMAs.
+    `operands`: None, or a bf16 CUDA tensor whose first 4096 values the
+    MFMA operands are drawn from (the sustained clock depends on the data).
     Returns {"tflops", "clock_ghz", "mfma_per_wave", "launches"}."""
     import torch
+
+    if operands is not None:
+        if operands.dtype != torch.bfloat16 or not operands.is_cuda or operands.numel() < 4096:
+            raise ValueError("operands must be a CUDA bf16 tensor of at least 4096 values")
+        operands = operands.reshape(-1)[:4096].contiguous()
 
     nbytes = lib().fa_mfma_peak_records_bytes()
     if nbytes == 0:
         raise FaError(0, "fa_mfma_peak_records_bytes (no device)")
     records = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
     tf, ghz = ctypes.c_double(), ctypes.c_double()
-    st = lib().fa_mfma_peak(mfma_per_wave, launches, _ptr(records), ctypes.byref(tf), ctypes.byref(ghz),
-                            _stream(stream))
+    st = lib().fa_mfma_peak(_ptr(operands), mfma_per_wave, launches, _ptr(records), ctypes.byref(tf),
+                            ctypes.byref(ghz), _stream(stream))
     _check(st, "fa_mfma_peak")
     return {"tflops": tf.value, "clock_ghz": ghz.value, "mfma_per_wave": mfma_per_wave - mfma_per_wave % 8,
             "launches": launches}

@@ -26,22 +26,38 @@ constexpr int kCalibMfmaPerIter = 8;     // unrolled MFMAs per loop iteration
 constexpr int kCalibRecordWords = 4;     // uint64 words per workgroup record
 constexpr double kFlopsPerMfma = 2.0 * 32 * 32 * 16;
 
+constexpr int kCalibOperands = 4096;      // bf16 values of a caller's operand pool
+
 // Each workgroup writes {shader ticks, wall-clock ticks, accumulator-sum
 // bits, 0} from thread 0; the sum keeps every MFMA live.
-__global__ __launch_bounds__(kCalibThreads) void mfma_peak_kernel(uint64_t* __restrict__ records, int iters)
+// The sustained clock under full MFMA load depends on the operand data (the
+// matrix pipes' switching power): measured on MI355X, zeros run at 2.39 GHz,
+// uniform[-1,1) bf16 at 1.94 GHz and N(0, 3^2) bf16 at 1.76 GHz. `ops`
+// (kCalibOperands bf16 values, e.g. taken from a workload's Q and K) sets
+// the data; without it, hashed mantissas and signs in [-1, -0.5] U [0.5, 1].
+__global__ __launch_bounds__(kCalibThreads) void mfma_peak_kernel(uint64_t* __restrict__ records,
+                                                                  const uint16_t* __restrict__ ops, int iters)
 {
-    // Operands with hashed mantissas and signs in [-1, -0.5] U [0.5, 1], so
-    // the matrix pipes switch about as much as on attention data (a clock
-    // under power limits depends on it).
     const uint32_t lane = threadIdx.x & 63;
     fa::bf16x8 a, b;
 #pragma unroll
     for (int e = 0; e < 8; ++e)
     {
-        const uint32_t ha = (lane * 8u + e) * 2654435761u;
-        const uint32_t hb = (lane * 8u + e + 512u) * 2246822519u;
-        a[e] = __builtin_bit_cast(__bf16, static_cast<uint16_t>(0x3f00u | ((ha >> 16) & 0x807fu)));
-        b[e] = __builtin_bit_cast(__bf16, static_cast<uint16_t>(0x3f00u | ((hb >> 16) & 0x807fu)));
+        uint16_t ba, bb;
+        if (ops)
+        {
+            ba = ops[(lane * 8u + e) % kCalibOperands];
+            bb = ops[(lane * 8u + e + kCalibOperands / 2) % kCalibOperands];
+        }
+        else
+        {
+            const uint32_t ha = (lane * 8u + e) * 2654435761u;
+            const uint32_t hb = (lane * 8u + e + 512u) * 2246822519u;
+            ba = static_cast<uint16_t>(0x3f00u | ((ha >> 16) & 0x807fu));
+            bb = static_cast<uint16_t>(0x3f00u | ((hb >> 16) & 0x807fu));
+        }
+        a[e] = __builtin_bit_cast(__bf16, ba);
+        b[e] = __builtin_bit_cast(__bf16, bb);
     }
     fa::f32x16 acc0 = {}, acc1 = {}, acc2 = {}, acc3 = {};
     const uint64_t t0 = __builtin_amdgcn_s_memtime();
@@ -93,8 +109,10 @@ size_t fa_mfma_peak_records_bytes(void)
     return static_cast<size_t>(cus) * kCalibRecordWords * sizeof(uint64_t);
 }
 
-int fa_mfma_peak(int mfma_per_wave, int launches, void* records, double* tflops, double* clock_ghz, void* stream)
+int fa_mfma_peak(const void* operands, int mfma_per_wave, int launches, void* records, double* tflops, double* clock_ghz,
+                 void* stream)
 {
+    const auto* ops = static_cast<const uint16_t*>(operands);
     if (!records || !tflops || !clock_ghz || mfma_per_wave < kCalibMfmaPerIter || launches < 1)
         return fa::record_status(hipErrorInvalidValue);
     *tflops = 0.0;
@@ -119,11 +137,11 @@ int fa_mfma_peak(int mfma_per_wave, int launches, void* records, double* tflops,
     for (hipEvent_t& e : ev)
         if ((st = hipEventCreate(&e)) != hipSuccess) return finish(st);
     // One untimed launch (code load, clock ramp), then the timed ones.
-    if ((st = fa::launch_kernel(mfma_peak_kernel, dim3(cus), dim3(kCalibThreads), s, rec, iters)) != hipSuccess)
+    if ((st = fa::launch_kernel(mfma_peak_kernel, dim3(cus), dim3(kCalibThreads), s, rec, ops, iters)) != hipSuccess)
         return finish(st);
     if ((st = hipEventRecord(ev[0], s)) != hipSuccess) return finish(st);
     for (int l = 0; l < launches; ++l)
-        if ((st = fa::launch_kernel(mfma_peak_kernel, dim3(cus), dim3(kCalibThreads), s, rec, iters)) != hipSuccess)
+        if ((st = fa::launch_kernel(mfma_peak_kernel, dim3(cus), dim3(kCalibThreads), s, rec, ops, iters)) != hipSuccess)
             return finish(st);
     if ((st = hipEventRecord(ev[1], s)) != hipSuccess) return finish(st);
     if ((st = hipEventSynchronize(ev[1])) != hipSuccess) return finish(st);

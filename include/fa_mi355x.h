@@ -252,14 +252,19 @@ int fa_time_batch(int which, const void* q, const void* k, const void* v, void* 
  * `mfma_per_wave` (>= 8; rounded down to a multiple of 8) back-to-back
  * v_mfma_f32_32x32x16_bf16 on four independent accumulators. `records` is a
  * device buffer of fa_mfma_peak_records_bytes() bytes (the kernel's per-
- * workgroup clock stamps). Synchronises `stream`. *tflops: the rate over the
- * timed launches; *clock_ghz: the median shader clock of the last launch
+ * workgroup clock stamps). `operands` is NULL (hashed bf16 values in
+ * [-1, -0.5] U [0.5, 1]) or a device pointer to 4096 bf16 values the MFMA
+ * operands are drawn from (a workload's own Q and K, say): the clock the
+ * device holds under this load depends on the data's switching power
+ * (measured on MI355X: zeros 2.39 GHz, uniform[-1,1) 1.94 GHz, N(0, 3^2)
+ * 1.76 GHz). Synchronises `stream`. *tflops: the rate over the timed
+ * launches; *clock_ghz: the median shader clock of the last launch
  * (s_memtime ticks over s_memrealtime wall time). For bench.py's
  * roofline.sustained_peak: the published 2.5 PFLOP/s assumes 2.4 GHz, which
- * the device does not hold under full MFMA load. */
+ * the device holds under full MFMA load only for low-activity data. */
 size_t fa_mfma_peak_records_bytes(void);
-int fa_mfma_peak(int mfma_per_wave, int launches, void* records, double* tflops, double* clock_ghz,
-                 void* stream);
+int fa_mfma_peak(const void* operands, int mfma_per_wave, int launches, void* records, double* tflops,
+                 double* clock_ghz, void* stream);
 
 /* Library identification: "gfx950" and the build's kernel configuration. */
 const char* fa_build_info(void);

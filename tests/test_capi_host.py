@@ -216,6 +216,19 @@ def test_argument_validation_before_launch(fa_lib):
         fa_lib.launch_attention_tensorcore_v3(None, fake, fake, fake, (1, 1, 64, 64), False, stream=0)
 
 
+def test_calibration_rejects_bad_arguments_before_any_device_call(fa_lib):
+    """fa_mfma_peak checks its arguments on the host first (no launch)."""
+    import ctypes
+
+    L = fa_lib.lib()
+    tf, ghz = ctypes.c_double(), ctypes.c_double()
+    fake = 0x10000
+    assert L.fa_mfma_peak(None, 4, 1, fake, ctypes.byref(tf), ctypes.byref(ghz), None) == 1  # < 8 MFMAs per wave
+    assert L.fa_mfma_peak(None, 64, 0, fake, ctypes.byref(tf), ctypes.byref(ghz), None) == 1  # no launch
+    assert L.fa_mfma_peak(None, 64, 1, None, ctypes.byref(tf), ctypes.byref(ghz), None) == 1  # no records
+    assert fa_lib.get_last_error() == 1
+
+
 def test_query_unsupported_needs_no_gpu(fa_lib):
     info = fa_lib.query_tensorcore_v3(96)
     assert info["supported"] == 0
