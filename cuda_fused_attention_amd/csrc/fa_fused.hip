@@ -261,6 +261,18 @@ __device__ __forceinline__ void dma16(i32x4 rsrc, uint32_t voff, uint32_t lds)
 #pragma clang diagnostic pop
 }
 
+// 16 bytes of O to global memory as a streaming (non-temporal) store. O is
+// written once and read by nothing in the kernel; keeping its lines out of
+// the L2 shortens the end of a launch, when every workgroup writes its rows
+// at once (measured back to back: c3 -3 %, c2 causal -3 %, the
+// (2,8,2048,128) dense headline -1.3 %, c2 -0.8 %, long shapes unchanged; the
+// same hint on the Q copies gained nothing).
+__device__ __forceinline__ void store_o16(uint16_t* p, uint4 v)
+{
+    typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+    __builtin_nontemporal_store(u32x4{v.x, v.y, v.z, v.w}, reinterpret_cast<u32x4*>(p));
+}
+
 __device__ __forceinline__ uint32_t lds_addr(const uint16_t* p)
 {
     return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void*)(p)));
@@ -1062,8 +1074,7 @@ __attribute__((amdgpu_waves_per_eu(kMinWavesPerSimd<D, kGroups, kCausal>, 8))) v
             const int row = x / kColChunks;
             const int c = x % kColChunks;
             const uint4 chunk = *reinterpret_cast<const uint4*>(obuf + row * kCols + ((c ^ (row & (kColChunks - 1))) * 8));
-            if (row0 + row < n)
-                *reinterpret_cast<uint4*>(o + slab_off + static_cast<size_t>(row0 + row) * D + kFirstDb * 32 + c * 8) = chunk;
+            if (row0 + row < n) store_o16(o + slab_off + static_cast<size_t>(row0 + row) * D + kFirstDb * 32 + c * 8, chunk);
         }
     };
 
@@ -1223,7 +1234,8 @@ __attribute__((amdgpu_waves_per_eu(kMinWavesPerSimd<D, kGroups, kCausal>, 8))) v
     // the other half of its O^T, its exponent base and its partial row sums
     // to the other group's wave with the same slot through LDS, folds the
     // half it receives into its own, normalises, and stores its half of the
-    // rows. All DMAs have landed (every wave drained its own before the last
+    // rows (at head_dim 64: half of the rows, whole, after one more barrier).
+    // All DMAs have landed (every wave drained its own before the last
     // barrier), so the stage area is free.
     auto finish = [&](auto gtag) {
         constexpr int G = decltype(gtag)::value;
@@ -1268,8 +1280,39 @@ __attribute__((amdgpu_waves_per_eu(kMinWavesPerSimd<D, kGroups, kCausal>, 8))) v
             }
         const float inv = inv_row_sum(l);
         wait_vm_lgkm0<0>();  // received values are in registers before the area is reused
-        store_rows(std::integral_constant<int, kKeep>{}, std::integral_constant<int, kHalfDb>{},
-                   reinterpret_cast<uint16_t*>(x_recv), inv, wq0);
+        if constexpr (D == 64)
+        {
+            // A 32-dim half is 64 bytes of a 128-byte row: both waves of the
+            // slot put their halves into the slot's Q rows (unused since the
+            // walk) as one row-major 32 x 64 bf16 block with XOR-swizzled
+            // 16-byte chunks, then each stores 16 whole rows, so the
+            // streaming stores write whole lines (separate 64-byte halves
+            // measured 25 % more HBM write bytes).
+            uint16_t* const rbuf = lds + C::kLdsElems + slot * 32 * D;
+#pragma unroll
+            for (int g4 = 0; g4 < 4; ++g4)
+            {
+                uint2 packed;
+                packed.x = fa::pack_bf16x2(f.o[kKeep][4 * g4 + 0] * inv, f.o[kKeep][4 * g4 + 1] * inv);
+                packed.y = fa::pack_bf16x2(f.o[kKeep][4 * g4 + 2] * inv, f.o[kKeep][4 * g4 + 3] * inv);
+                const int chunk = (4 * kKeep + g4) ^ (i & 7);
+                *reinterpret_cast<uint2*>(rbuf + i * D + chunk * 8 + 4 * h) = packed;
+            }
+            wait_vm_lgkm0<0>();
+            barrier();
+#pragma unroll
+            for (int u = 0; u < 2; ++u)
+            {
+                const int x = u * 64 + lane;
+                const int row = 16 * G + x / 8;
+                const int c = x % 8;
+                const uint4 chunk = *reinterpret_cast<const uint4*>(rbuf + row * D + ((c ^ (row & 7)) * 8));
+                if (wq0 + row < n) store_o16(o + slab_off + static_cast<size_t>(wq0 + row) * D + c * 8, chunk);
+            }
+        }
+        else
+            store_rows(std::integral_constant<int, kKeep>{}, std::integral_constant<int, kHalfDb>{},
+                       reinterpret_cast<uint16_t*>(x_recv), inv, wq0);
     };
     if constexpr (kGroups == 4)
     {
@@ -1321,7 +1364,11 @@ __attribute__((amdgpu_waves_per_eu(kMinWavesPerSimd<D, kGroups, kCausal>, 8))) v
     }
     if (grp_s == 0) finish(std::integral_constant<int, 0>{});
     else if (grp_s == 1 || kGroups == 2) finish(std::integral_constant<int, 1>{});
-    else barrier();  // groups 2 and 3: the barrier inside finish
+    else
+    {
+        barrier();  // groups 2 and 3: the barrier inside finish
+        if constexpr (D == 64) barrier();  // and the one before its whole-row stores
+    }
     }
 }
 
