@@ -1049,7 +1049,8 @@ __attribute__((amdgpu_waves_per_eu(kMinWavesPerSimd<D, kGroups, kCausal>, 8))) v
     // rows by `inv` and store them (head dims 32*kFirstDb ..): O^T (lane =
     // query) is transposed through `obuf` (32 rows of 32*kNumDb bf16, only
     // this wave touches it now) into row-major bf16 with XOR-swizzled 16-byte
-    // chunks, then stored as contiguous 16-byte pieces of the rows.
+    // chunks, then stored as contiguous 16-byte pieces of the rows
+    // (streaming stores, store_o16).
     auto store_rows = [&](auto first_tag, auto num_tag, uint16_t* obuf, float inv, int row0) {
         constexpr int kFirstDb = decltype(first_tag)::value;
         constexpr int kNumDb = decltype(num_tag)::value;
@@ -1320,7 +1321,7 @@ __attribute__((amdgpu_waves_per_eu(kMinWavesPerSimd<D, kGroups, kCausal>, 8))) v
         // exponent base, partial row sums) to the group-0 / group-1 wave with
         // the same slot, which folds it into its own (the same rescale as
         // between steps); then groups 0 and 1 merge and store as above, and
-        // groups 2 and 3 only join that merge's barrier. The hand-over area
+        // groups 2 and 3 only join that merge's barriers. The hand-over area
         // lies past the one `finish` uses, in the free stage area.
         constexpr int kFull = (D / 32) * 16 * 64;                     // one wave's O^T
         constexpr int kSlotFloats = kFull + 128;
