@@ -1,4 +1,4 @@
-"""Maximum-size addressing: tensors past 4 GiB.
+"""Maximum sizes: tensors past 4 GiB, and a 65536-key sequence.
 
 (1, 8192, 4096, 64) bf16 is 4 GiB per tensor, so the last (batch, head) slabs
 start beyond 2^32 bytes: every slab offset, K/V descriptor base and output row
@@ -11,7 +11,7 @@ slab the kernel skips fails the check."""
 import numpy as np
 import pytest
 
-from gpu_common import from_dev, nan_like, run, say, to_dev
+from gpu_common import FUSED_KERNELS, HOST_THREADS, from_dev, kernels_for, nan_like, run, say, to_dev
 from test_gpu_parity import check, fa  # noqa: F401 (fa: fixture)
 
 pytestmark = [pytest.mark.gpu, pytest.mark.slow]
@@ -60,3 +60,28 @@ def test_list_layout_long_sequence(fa, oracle_mod):
     pinned = from_dev(run(fa, "v3_128x4", *(to_dev(x) for x in (qb, kb, vb)), True))
     assert cus != 256 or np.array_equal(got, pinned)
     check(oracle_mod, pinned, ref, "list long pinned")
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_sequence_65536(fa, oracle_mod, D):
+    """N = 65536 in one slab, four times the longest BASELINE sequence (c5):
+    2048 K/V tiles in a walk. Dense on uniform inputs, and causal on the
+    stress family (Q, K ~ N(0, 3^2)), whose logits keep raising the row
+    maximum along the whole walk, so the exponent base moves again and again.
+    Every fused configuration. The first and last query tiles and 64 seeded
+    random rows are checked against the FP64 oracle, and every output element
+    must be finite after the NaN prefill."""
+    B, H, N = 1, 1, 65536
+    rows = oracle_mod.sample_rows(B, H, N)
+    for family, causal in (("uniform", False), ("stress", True)):
+        qb, kb, vb = oracle_mod.make_inputs(B, H, N, D, family, seeds={"q": 71 + D, "k": 72 + D, "v": 73 + D})
+        ref = oracle_mod.attention(qb, kb, vb, causal, rows=rows, threads=HOST_THREADS)
+        q, k, v = to_dev(qb), to_dev(kb), to_dev(vb)
+        for kernel in kernels_for(D, FUSED_KERNELS):
+            say("seq 65536", kernel, D, family, causal)
+            out = from_dev(run(fa, kernel, q, k, v, causal)).reshape(-1, D)
+            assert int(np.count_nonzero((out & 0x7F80) == 0x7F80)) == 0, (kernel, causal)
+            acc = check(oracle_mod, out[rows], ref, f"seq 65536 {kernel} D={D} {family} causal={causal}")
+            print(f"seq 65536 {kernel} D={D} {family} causal={causal} rows {len(rows)} ulp={acc.ulp:.2f} "
+                  f"row_scaled={acc.row_scaled:.2e}")
+        del q, k, v
