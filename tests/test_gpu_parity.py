@@ -167,6 +167,37 @@ def test_base_moves(fa, oracle_mod):
                               f"base moves {name} {kernel} {(N, D, causal)}")
 
 
+def bf16_is_nan(bits):
+    return ((bits & 0x7F80) == 0x7F80) & ((bits & 0x7F) != 0)
+
+
+def test_non_finite_inputs(fa, oracle_mod):
+    """A NaN in one query row (head 0, row 5) and in one key (head 1, key
+    200). Exactly the rows whose FP64 oracle output is NaN come out NaN, in
+    every element, and every other row passes the gate. Causal rows 192-199
+    share key 200's diagonal tile without seeing it: the mask replaces its
+    score rather than adding to it, so they stay finite. (A non-finite V is
+    not meaningful here: a masked or underflowed P of 0 times Inf or NaN is
+    NaN in any matrix product, while the oracle never multiplies it.)"""
+    B, H, N = 1, 2, 300
+    for D in (64, 128):
+        q, k, v = oracle_mod.make_inputs(B, H, N, D, seeds={"q": 81, "k": 82, "v": 83})
+        q[0, 0, 5, 7] = 0x7FC0
+        k[0, 1, 200, 3] = 0x7FC0
+        for causal in (False, True):
+            ref = oracle_mod.attention(q, k, v, causal, threads=HOST_THREADS).reshape(-1, D)
+            nan_rows = np.isnan(ref).any(axis=1)
+            assert np.isnan(ref[nan_rows]).all()
+            expected = {5} | set(range(N + (200 if causal else 0), 2 * N))
+            assert set(np.flatnonzero(nan_rows).tolist()) == expected
+            for kernel in kernels_for(D):
+                say("non-finite", kernel, D, causal)
+                got = run_bits(fa, kernel, q, k, v, causal).reshape(-1, D)
+                assert bf16_is_nan(got[nan_rows]).all(), (kernel, D, causal)
+                assert not bf16_is_nan(got[~nan_rows]).any(), (kernel, D, causal)
+                check(oracle_mod, got[~nan_rows], ref[~nan_rows], f"non-finite {kernel} {(D, causal)}")
+
+
 def test_v3_and_v3b_agree(fa, oracle_mod):
     """The 128-row (v3_128) and 64-row (v3b) configurations. Dense: each wave
     computes its 32 rows identically whatever the workgroup size (both
