@@ -172,24 +172,33 @@ def bf16_is_nan(bits):
 
 
 def test_non_finite_inputs(fa, oracle_mod):
-    """A NaN in one query row (head 0, row 5) and in one key (head 1, key
-    200). Exactly the rows whose FP64 oracle output is NaN come out NaN, in
-    every element, and every other row passes the gate. Causal rows 192-199
-    share key 200's diagonal tile without seeing it: the mask replaces its
-    score rather than adding to it, so they stay finite. (A non-finite V is
-    not meaningful here: a masked or underflowed P of 0 times Inf or NaN is
-    NaN in any matrix product, while the oracle never multiplies it.)"""
+    """A NaN in one query row (head 0, row 5), a NaN in one key (head 1, key
+    200) and +Inf in one element of another key (head 0, key 100, dim 3).
+    Exactly the rows whose FP64 oracle output is NaN come out NaN, in every
+    element, and every other row passes the gate. The Inf key scores +Inf
+    for the rows with q[3] > 0 (NaN outputs: the exponent base moves to
+    infinity, as the oracle's max does), NaN where q[3] is zero, and -Inf
+    where q[3] < 0 (P = 0: those rows stay finite). Causal rows that share a
+    bad key's diagonal tile without seeing it stay finite: the mask replaces
+    scores rather than adding to them. (A non-finite V is not meaningful
+    here: a masked or underflowed P of 0 times Inf or NaN is NaN in any
+    matrix product, while the oracle never multiplies it.)"""
     B, H, N = 1, 2, 300
     for D in (64, 128):
         q, k, v = oracle_mod.make_inputs(B, H, N, D, seeds={"q": 81, "k": 82, "v": 83})
         q[0, 0, 5, 7] = 0x7FC0
         k[0, 1, 200, 3] = 0x7FC0
+        k[0, 0, 100, 3] = 0x7F80
+        q3 = oracle_mod.bf16_to_f32(q[0, 0, :, 3])
         for causal in (False, True):
             ref = oracle_mod.attention(q, k, v, causal, threads=HOST_THREADS).reshape(-1, D)
             nan_rows = np.isnan(ref).any(axis=1)
             assert np.isnan(ref[nan_rows]).all()
-            expected = {5} | set(range(N + (200 if causal else 0), 2 * N))
+            sees_inf = np.arange(N) >= (100 if causal else 0)
+            expected = ({5} | set(np.flatnonzero(sees_inf & (q3 >= 0)).tolist())
+                        | set(range(N + (200 if causal else 0), 2 * N)))
             assert set(np.flatnonzero(nan_rows).tolist()) == expected
+            assert (sees_inf & (q3 < 0)).sum() > 50  # rows that see -Inf and stay finite
             for kernel in kernels_for(D):
                 say("non-finite", kernel, D, causal)
                 got = run_bits(fa, kernel, q, k, v, causal).reshape(-1, D)
