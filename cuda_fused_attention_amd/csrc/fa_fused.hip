@@ -56,10 +56,10 @@
 //   * Scores stay in the log2 domain (scale*log2(e) folded into one FMA before
 //     v_exp_f32). Row sums accumulate the bf16-rounded P with
 //     v_dot2_f32_bf16, the same weights the PV MFMA uses. The exponent base
-//     is set from the first tile's row max (plus headroom); afterwards no
-//     per-tile row max is taken: the base is raised only when a tile's
-//     partial row sum exceeds 2^16, and then O and the row sum are rescaled
-//     and the tile recomputed. Every P the matrix pipe consumes is <= 2^16.
+//     is set to the first tile's row max; afterwards no per-tile row max is
+//     taken: the base is raised only when a tile's partial row sum exceeds
+//     2^64, and then O and the row sum are rescaled and the tile
+//     recomputed. Every P the matrix pipe consumes is <= 2^64.
 //   * Causal: a wave skips tiles wholly above its diagonal, and only tiles
 //     that cross the diagonal or the sequence end pay for the per-element
 //     mask (-inf). When the grid fits one round on the device, a two-group
@@ -104,15 +104,19 @@ constexpr int kTileKV = fa::kFusedTileKV;  // keys per LDS tile
 constexpr int kStages = fa::kFusedStages;  // LDS stages per tensor per group
 // A tile's partial row sum above kSumLimit moves the exponent base; a new
 // base is placed kBaseHeadroom (log2 units) above the row max, so a row's
-// max must grow by about kBaseHeadroom + 12 before the next move. Every P is
-// then at most 2^16, and after a move at most 2^-48: that leaves 78 binary
-// orders of magnitude below the row max before fp32 denormals, and keys
-// further down weigh less than 2^-78 of the largest. Moves are expensive
-// (the tile is recomputed), and inputs with large, still-growing logits
-// (N(0, 3^2) Q and K) made them frequent with a tight limit and no headroom:
-// c5 went from 1.40 ms to 0.955 ms with these values.
-constexpr float kSumLimit = 65536.0f;
-constexpr float kBaseHeadroom = 48.0f;
+// max must grow by about kBaseHeadroom + 60 before the next move. Moves are
+// expensive (the tile is recomputed), and inputs with large, still-growing
+// logits (N(0, 3^2) Q and K) made them frequent with a tight limit: c5 went
+// from 1.40 ms (limit 2^8) to 0.955 ms once a move needed ~60 log2 units of
+// growth. That allowance sits in the limit, not in a headroom above the
+// max: right after a move P <= 1, as in a plain online softmax, so P V keeps
+// fp32's whole range for V (measured: V scaled by 2^-130 to 2^115 matches
+// the FP64 reference). With the base 48 units above the max and a 2^16
+// limit (the same move frequency) every P was at most 2^-48 after a move,
+// and P V underflowed for |V| below ~2^-78. P only exceeds 1 while a row's
+// max grows, and never exceeds 2^64.
+constexpr float kSumLimit = 18446744073709551616.0f;  // 2^64
+constexpr float kBaseHeadroom = 0.0f;
 
 // How the kWpg waves of one group share the copies of a K or V tile.
 // A copy moves 1 KiB (64 lanes x 16 B), or 512 B from the low 32 lanes when

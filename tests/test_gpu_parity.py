@@ -132,11 +132,11 @@ def test_causal_work_layouts(fa, oracle_mod):
 def growing_logit_inputs(oracle_mod, B, H, N, D, seed, top=60.0):
     """Q ~ 0.5 + noise, K rows growing linearly along the sequence: every
     query's logits rise key after key, to about `top` at the last key. The
-    fused kernels move their exponent base when a tile's row sum passes 2^16,
-    and place it 48 log2 units above the row max, so a move follows about
-    every 64 log2 units (44 natural) of growth: `top` 60 moves it once or
-    twice per row, `top` 500 on every tile at N 256 and every third tile at N
-    1000. The same keys in falling order (largest first) never move it."""
+    fused kernels move their exponent base to the row max when a tile's row
+    sum passes 2^64, so a move follows about every 60-64 log2 units (about
+    44 natural) of growth: `top` 60 moves it once or twice per row, `top` 500
+    on every tile at N 256 and every third tile at N 1000. The same keys in
+    falling order (largest first) never move it."""
     rng = np.random.default_rng(seed)
     kappa = 2.0 * top / np.sqrt(D)  # scale * D * 0.5 * kappa = top at the last key
     ramp = kappa * np.arange(N, dtype=np.float64) / N
@@ -165,6 +165,32 @@ def test_base_moves(fa, oracle_mod):
                         say("base moves", name, kernel, N, D, causal)
                         check(oracle_mod, run_bits(fa, kernel, qq, kk, vv, causal), ref,
                               f"base moves {name} {kernel} {(N, D, causal)}")
+
+
+def test_value_range(fa, oracle_mod):
+    """V scaled across bf16's range (2^-120, subnormal 2^-130, 2^100, 2^115)
+    and Q, K scaled to subnormals or to opposite extremes, against the
+    oracle, every kernel, both head dims and masks. The softmax weights do
+    not depend on V's scale, so every case exercises the P V products at the
+    edges of fp32: the fused kernels keep P <= 1 outside base moves, so
+    their products neither underflow for tiny V nor overflow for huge V."""
+    B, H, N = 1, 2, 300
+    for D in (64, 128):
+        q, k, v = oracle_mod.make_inputs(B, H, N, D, seeds={"q": 1, "k": 2, "v": 3})
+        qf, kf, vf = (oracle_mod.bf16_to_f32(x).astype(np.float64) for x in (q, k, v))
+        cases = [("v 2^-120", q, k, oracle_mod.bf16_bits(vf * 2.0 ** -120)),
+                 ("v 2^-130", q, k, oracle_mod.bf16_bits(vf * 2.0 ** -130)),
+                 ("v 2^100", q, k, oracle_mod.bf16_bits(vf * 2.0 ** 100)),
+                 ("v 2^115", q, k, oracle_mod.bf16_bits(vf * 2.0 ** 115)),
+                 ("qk 2^-130", oracle_mod.bf16_bits(qf * 2.0 ** -130), oracle_mod.bf16_bits(kf * 2.0 ** -130), v),
+                 ("q 2^100 k 2^-128", oracle_mod.bf16_bits(qf * 2.0 ** 100), oracle_mod.bf16_bits(kf * 2.0 ** -128), v)]
+        for name, qq, kk, vv in cases:
+            for causal in (False, True):
+                ref = oracle_mod.attention(qq, kk, vv, causal, threads=HOST_THREADS)
+                for kernel in kernels_for(D):
+                    say("value range", name, kernel, D, causal)
+                    check(oracle_mod, run_bits(fa, kernel, qq, kk, vv, causal), ref,
+                          f"value range {name} {kernel} {(D, causal)}")
 
 
 def bf16_is_nan(bits):
