@@ -59,7 +59,9 @@
 //     is set to the first tile's row max; afterwards no per-tile row max is
 //     taken: the base is raised only when a tile's partial row sum exceeds
 //     2^64, and then O and the row sum are rescaled and the tile
-//     recomputed. Every P the matrix pipe consumes is <= 2^64.
+//     recomputed. Every P the matrix pipe consumes is <= 2^64. Waves whose
+//     base reaches 2^28 in magnitude (logits far beyond any softmax input)
+//     recompute every tile from rounded products instead.
 //   * Causal: a wave skips tiles wholly above its diagonal, and only tiles
 //     that cross the diagonal or the sequence end pay for the per-element
 //     mask (-inf). When the grid fits one round on the device, a two-group
@@ -426,11 +428,12 @@ __device__ __forceinline__ void pv_part(Frag<D>& f, const bf16x8 (&va)[D / 32][2
 }
 
 // Row state of the online softmax (per lane: one query, half of its keys).
-// The exponent base starts at a large finite negative value rather than
-// -inf: a row that has seen no key yet keeps it (and l = 0), and every
-// update below needs no special case (exp2 of base differences is 0 or 1
-// there, masked scores are -inf and give P = 0).
-constexpr float kEmptyBase = -1.0e30f;
+// The exponent base starts at the most negative finite float rather than
+// -inf: a row that has seen no key yet keeps it (and l = 0), every finite
+// scaled score is at least as large, and every update below needs no
+// special case (exp2 of base differences is 0 or 1 there, masked scores are
+// -inf and give P = 0).
+constexpr float kEmptyBase = -3.40282347e38f;  // -FLT_MAX
 
 struct RowState
 {
@@ -453,6 +456,40 @@ __device__ __forceinline__ void exp_part(const f32x16& s, bf16x8& p, float m, fl
         const fa::bf16x2 pair = {p[kPos + e], p[kPos + e + 1]};
         sum = __builtin_amdgcn_fdot2_f32_bf16(pair, ones, sum, false);
     }
+}
+
+// The rare path's exponentials: the product is rounded before the base is
+// subtracted, so the score that set the base gets P = exp2(0) = 1 exactly
+// (the base is the rounded product of the row max), whatever its magnitude.
+template <int kFirst, int kPos, int kCount>
+__device__ __forceinline__ void exp_part_rounded(const f32x16& s, bf16x8& p, float m, float c_log2, float& sum)
+{
+#pragma unroll
+    for (int e = 0; e < kCount; ++e)
+    {
+#pragma clang fp contract(off)
+        const float x = s[kFirst + e] * c_log2 - m;
+        p[kPos + e] = static_cast<__bf16>(__builtin_amdgcn_exp2f(x));
+    }
+    const fa::bf16x2 ones = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
+#pragma unroll
+    for (int e = 0; e < kCount; e += 2)
+    {
+        const fa::bf16x2 pair = {p[kPos + e], p[kPos + e + 1]};
+        sum = __builtin_amdgcn_fdot2_f32_bf16(pair, ones, sum, false);
+    }
+}
+
+// A base of magnitude 2^28 or more (log2 units) has an fp32 spacing of 32 or
+// more. The fused exponent subtracts it from the exact product, so the row
+// max can come out up to half that spacing above it, and from 2^30 on, P
+// overflows. Such waves lower their move limit to -1: every later tile
+// takes the recompute path (exp_part_rounded). Rows without keys keep the
+// empty base and do not count.
+constexpr float kCoarseBase = 268435456.0f;  // 2^28
+__device__ __forceinline__ bool base_too_coarse(float m)
+{
+    return m != kEmptyBase && __builtin_fabsf(m) >= kCoarseBase;
 }
 
 // Per-element mask of a tile's scores: key offset of element r is
@@ -805,6 +842,13 @@ __attribute__((amdgpu_waves_per_eu(kMinWavesPerSimd<D, kGroups, kCausal>, 8))) v
         bf16x8 ka[D / 16];
         bf16x8 va[D / 32][2];
         float tsum = 0.0f;  // partial row sum of the tile being exponentiated
+        // The move limit's bits, wave-uniform (an SGPR): kSumLimit, or -1.0f
+        // once the base is too coarse (every later tile is recomputed).
+        int limit_bits = __builtin_bit_cast(int, kSumLimit);
+        auto note_base = [&](float m) {
+            if (__any(base_too_coarse(m))) limit_bits = __builtin_bit_cast(int, -1.0f);
+            limit_bits = __builtin_amdgcn_readfirstlane(limit_bits);
+        };
         if (lw >= 0)
         {
             load_k_ops<D>(lds, f, ka);
@@ -814,6 +858,7 @@ __attribute__((amdgpu_waves_per_eu(kMinWavesPerSimd<D, kGroups, kCausal>, 8))) v
             // O and l are still zero: the base moves without rescaling.
             rs.m = __builtin_elementwise_maximum(rs.m, row_max_raw(sbuf[0]) * c_log2 + kBaseHeadroom);
             exp_part<0, 0, 8>(sbuf[0], p_lo[0], rs.m, c_log2, tsum);
+            note_base(rs.m);
         }
         wait_vm_lgkm0<0>();
         barrier();  // every prologue tile resident; K_0's stage is free
@@ -872,11 +917,12 @@ __attribute__((amdgpu_waves_per_eu(kMinWavesPerSimd<D, kGroups, kCausal>, 8))) v
             const float m_new = __builtin_elementwise_maximum(rs.m, row_max_raw(st) * c_log2 + kBaseHeadroom);
             const float alpha = __builtin_amdgcn_exp2f(rs.m - m_new);
             rs.m = m_new;
+            note_base(m_new);
             rescale_o<D>(f, alpha);
             float sum = 0.0f;
             bf16x8 pr[2];
-            exp_part<0, 0, 8>(st, pr[0], rs.m, c_log2, sum);
-            exp_part<8, 0, 8>(st, pr[1], rs.m, c_log2, sum);
+            exp_part_rounded<0, 0, 8>(st, pr[0], rs.m, c_log2, sum);
+            exp_part_rounded<8, 0, 8>(st, pr[1], rs.m, c_log2, sum);
             rs.l = rs.l * alpha + sum;
             load_v_ops<D>(lds + (P % kStages) * C::kTileElems, f, va);
             pv_part<D, 0, D / 16>(f, va, pr);
@@ -919,7 +965,7 @@ __attribute__((amdgpu_waves_per_eu(kMinWavesPerSimd<D, kGroups, kCausal>, 8))) v
             // 64).
             const bool lead_b = kGroups > 1 && G >= kGroups / 2 && !kCausal;
             if (lead_b) __builtin_amdgcn_s_setprio(1);
-            const bool rare = __any(tsum > kSumLimit);
+            const bool rare = __any(tsum > __builtin_bit_cast(float, limit_bits));
             if (rare)
             {
                 // The empty volatile asm keeps this a branch (not selects on
@@ -982,6 +1028,7 @@ __attribute__((amdgpu_waves_per_eu(kMinWavesPerSimd<D, kGroups, kCausal>, 8))) v
             j_end = lw + 1;
             if (t_mask <= 0) mask_tile(sbuf[B ^ 1], dead_base);
             rs.m = __builtin_elementwise_maximum(kEmptyBase, row_max_raw(sbuf[B ^ 1]) * c_log2 + kBaseHeadroom);
+            note_base(rs.m);
             rs.l = 0.0f;
             tsum = 0.0f;
             exp_part<0, 0, 8>(sbuf[B ^ 1], p_lo[B ^ 1], rs.m, c_log2, tsum);

@@ -168,12 +168,17 @@ def test_base_moves(fa, oracle_mod):
 
 
 def test_value_range(fa, oracle_mod):
-    """V scaled across bf16's range (2^-120, subnormal 2^-130, 2^100, 2^115)
-    and Q, K scaled to subnormals or to opposite extremes, against the
-    oracle, every kernel, both head dims and masks. The softmax weights do
-    not depend on V's scale, so every case exercises the P V products at the
+    """V scaled across bf16's range (2^-120, subnormal 2^-130, 2^100, 2^115),
+    Q and K scaled to subnormals or to opposite extremes, and Q and K both
+    scaled by 2^12 to 2^56 (scores up to about 2^118), against the oracle,
+    every kernel, both head dims and masks. The softmax weights do not
+    depend on V's scale, so the V cases exercise the P V products at the
     edges of fp32: the fused kernels keep P <= 1 outside base moves, so
-    their products neither underflow for tiny V nor overflow for huge V."""
+    their products neither underflow for tiny V nor overflow for huge V.
+    Large Q and K push the exponent base past 2^28, where the fused
+    exponent's exact product minus the rounded base loses the row max, and
+    below the old empty-row sentinel; those waves recompute every tile from
+    rounded products."""
     B, H, N = 1, 2, 300
     for D in (64, 128):
         q, k, v = oracle_mod.make_inputs(B, H, N, D, seeds={"q": 1, "k": 2, "v": 3})
@@ -184,6 +189,8 @@ def test_value_range(fa, oracle_mod):
                  ("v 2^115", q, k, oracle_mod.bf16_bits(vf * 2.0 ** 115)),
                  ("qk 2^-130", oracle_mod.bf16_bits(qf * 2.0 ** -130), oracle_mod.bf16_bits(kf * 2.0 ** -130), v),
                  ("q 2^100 k 2^-128", oracle_mod.bf16_bits(qf * 2.0 ** 100), oracle_mod.bf16_bits(kf * 2.0 ** -128), v)]
+        cases += [(f"qk 2^{e}", oracle_mod.bf16_bits(qf * 2.0 ** e), oracle_mod.bf16_bits(kf * 2.0 ** e), v)
+                  for e in (12, 16, 24, 40, 56)]
         for name, qq, kk, vv in cases:
             for causal in (False, True):
                 ref = oracle_mod.attention(qq, kk, vv, causal, threads=HOST_THREADS)
