@@ -178,7 +178,8 @@ def test_value_range(fa, oracle_mod):
     Large Q and K push the exponent base past 2^28, where the fused
     exponent's exact product minus the rounded base loses the row max, and
     below the old empty-row sentinel; those waves recompute every tile from
-    rounded products."""
+    rounded products, also when the huge scores only start mid-walk (one
+    key, or the last quarter of the keys)."""
     B, H, N = 1, 2, 300
     for D in (64, 128):
         q, k, v = oracle_mod.make_inputs(B, H, N, D, seeds={"q": 1, "k": 2, "v": 3})
@@ -191,6 +192,11 @@ def test_value_range(fa, oracle_mod):
                  ("q 2^100 k 2^-128", oracle_mod.bf16_bits(qf * 2.0 ** 100), oracle_mod.bf16_bits(kf * 2.0 ** -128), v)]
         cases += [(f"qk 2^{e}", oracle_mod.bf16_bits(qf * 2.0 ** e), oracle_mod.bf16_bits(kf * 2.0 ** e), v)
                   for e in (12, 16, 24, 40, 56)]
+        # huge scores from the middle of the walk on: the base turns coarse after a move
+        one, late = kf.copy(), kf.copy()
+        one[:, :, N // 2, :] *= 2.0 ** 40
+        late[:, :, 3 * N // 4:, :] *= 2.0 ** 24
+        cases += [("one key 2^40", q, oracle_mod.bf16_bits(one), v), ("late keys 2^24", q, oracle_mod.bf16_bits(late), v)]
         for name, qq, kk, vv in cases:
             for causal in (False, True):
                 ref = oracle_mod.attention(qq, kk, vv, causal, threads=HOST_THREADS)
