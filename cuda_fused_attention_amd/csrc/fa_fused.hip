@@ -58,8 +58,8 @@
 //     v_dot2_f32_bf16, the same weights the PV MFMA uses. The exponent base
 //     is set to the first tile's row max; afterwards no per-tile row max is
 //     taken: the base is raised only when a tile's partial row sum exceeds
-//     2^64, and then O and the row sum are rescaled and the tile
-//     recomputed. Every P the matrix pipe consumes is <= 2^64. Waves whose
+//     2^48, and then O and the row sum are rescaled and the tile
+//     recomputed. Every P the matrix pipe consumes is <= 2^48. Waves whose
 //     base reaches 2^28 in magnitude (logits far beyond any softmax input)
 //     recompute every tile from rounded products instead.
 //   * Causal: a wave skips tiles wholly above its diagonal, and only tiles
@@ -106,18 +106,20 @@ constexpr int kTileKV = fa::kFusedTileKV;  // keys per LDS tile
 constexpr int kStages = fa::kFusedStages;  // LDS stages per tensor per group
 // A tile's partial row sum above kSumLimit moves the exponent base; a new
 // base is placed kBaseHeadroom (log2 units) above the row max, so a row's
-// max must grow by about kBaseHeadroom + 60 before the next move. Moves are
+// max must grow by about kBaseHeadroom + 44 before the next move. Moves are
 // expensive (the tile is recomputed), and inputs with large, still-growing
 // logits (N(0, 3^2) Q and K) made them frequent with a tight limit: c5 went
-// from 1.40 ms (limit 2^8) to 0.955 ms once a move needed ~60 log2 units of
-// growth. That allowance sits in the limit, not in a headroom above the
-// max: right after a move P <= 1, as in a plain online softmax, so P V keeps
-// fp32's whole range for V (measured: V scaled by 2^-130 to 2^115 matches
-// the FP64 reference). With the base 48 units above the max and a 2^16
-// limit (the same move frequency) every P was at most 2^-48 after a move,
-// and P V underflowed for |V| below ~2^-78. P only exceeds 1 while a row's
-// max grows, and never exceeds 2^64.
-constexpr float kSumLimit = 18446744073709551616.0f;  // 2^64
+// from 1.40 ms (limit 2^8) to 0.955 ms once a move needed ~44 or more log2
+// units of growth. That allowance sits in the limit, not in a headroom above
+// the max: right after a move P <= 1, as in a plain online softmax, so tiny
+// V keeps fp32's range (measured: V scaled down to 2^-130 matches the FP64
+// reference; with the base 48 units above the max every P was at most
+// 2^-48 after a move, and P V underflowed for |V| below ~2^-78). The price
+// is at the top: P exceeds 1 while a row's max grows, up to the limit, so
+// P V can overflow where the reference's would not once |V| passes about
+// 2^128 / (N * P). A 2^64 limit let V scaled by 2^72 overflow on fast-growing
+// logits; 2^48 keeps P <= 2^48 for 0.3 % on the c5 stress workload.
+constexpr float kSumLimit = 281474976710656.0f;  // 2^48
 constexpr float kBaseHeadroom = 0.0f;
 
 // How the kWpg waves of one group share the copies of a K or V tile.

@@ -133,10 +133,10 @@ def growing_logit_inputs(oracle_mod, B, H, N, D, seed, top=60.0):
     """Q ~ 0.5 + noise, K rows growing linearly along the sequence: every
     query's logits rise key after key, to about `top` at the last key. The
     fused kernels move their exponent base to the row max when a tile's row
-    sum passes 2^64, so a move follows about every 60-64 log2 units (about
-    44 natural) of growth: `top` 60 moves it once or twice per row, `top` 500
-    on every tile at N 256 and every third tile at N 1000. The same keys in
-    falling order (largest first) never move it."""
+    sum passes 2^48, so a move follows about every 44-48 log2 units (about
+    31 natural) of growth: `top` 60 moves it about twice per row, `top` 500
+    on every tile at N 256 and about every second tile at N 1000. The same
+    keys in falling order (largest first) never move it."""
     rng = np.random.default_rng(seed)
     kappa = 2.0 * top / np.sqrt(D)  # scale * D * 0.5 * kappa = top at the last key
     ramp = kappa * np.arange(N, dtype=np.float64) / N

@@ -70,3 +70,37 @@ def test_list_layout_length_sweep(fa, oracle_mod):
                 say("list sweep", kernel, N, causal)
                 acc = oracle_mod.compare(run_bits(fa, kernel, q, k, v, causal), ref)
                 assert acc.passed, f"list sweep {kernel} N={N} causal={causal}: {acc}"
+
+
+def random_scales(count, seed):
+    """(B, H, N, D, causal, a, b, c): Q, K and V scaled by 2^a, 2^b and 2^c.
+    a + b <= 8 keeps the logits within a few hundred (beyond that, fp32 score
+    rounding alone moves the softmax and no fp32 kernel matches the FP64
+    oracle); c spans 2^-120 to 2^60, inside the fused kernels' documented
+    range (P may grow to 2^48 between base moves)."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    for _ in range(count):
+        a = int(rng.integers(-30, 9))
+        b = int(rng.integers(-30, 9 - a)) if a < 8 else int(rng.integers(-30, 1))
+        cases.append((1, int(rng.integers(1, 4)), int(rng.integers(1, 700)), int(rng.choice([64, 128])),
+                      bool(rng.integers(0, 2)), a, b, int(rng.integers(-120, 61))))
+    return cases
+
+
+RANDOM_SCALES = random_scales(40, seed=20261203)
+
+
+def test_random_scales(fa, oracle_mod):
+    """Seeded random shapes with random power-of-two scales on Q, K and V:
+    logits from vanishing to a few hundred, V over 180 binary orders of
+    magnitude. Every kernel, every row against the oracle."""
+    for idx, (B, H, N, D, causal, a, b, c) in enumerate(RANDOM_SCALES):
+        q, k, v = oracle_mod.make_inputs(B, H, N, D, seeds={"q": 400 + idx, "k": 500 + idx, "v": 600 + idx})
+        qf, kf, vf = (oracle_mod.bf16_to_f32(x).astype(np.float64) for x in (q, k, v))
+        q, k, v = (oracle_mod.bf16_bits(x * 2.0 ** e) for x, e in ((qf, a), (kf, b), (vf, c)))
+        ref = oracle_mod.attention(q, k, v, causal, threads=HOST_THREADS)
+        for kernel in kernels_for(D):
+            say("random scales", idx, kernel, B, H, N, D, causal, a, b, c)
+            acc = oracle_mod.compare(run_bits(fa, kernel, q, k, v, causal), ref)
+            assert acc.passed, f"random scales {idx} {kernel} {(B, H, N, D, causal, a, b, c)}: {acc}"
