@@ -104,3 +104,45 @@ def test_random_scales(fa, oracle_mod):
             say("random scales", idx, kernel, B, H, N, D, causal, a, b, c)
             acc = oracle_mod.compare(run_bits(fa, kernel, q, k, v, causal), ref)
             assert acc.passed, f"random scales {idx} {kernel} {(B, H, N, D, causal, a, b, c)}: {acc}"
+
+
+def rising_logits(count, seed):
+    """(B, H, N, D, causal, a, r, c, ramp): Q scaled by 2^a, key j scaled by
+    ramp(j) rising from 1 to r along the sequence (linear, quadratic, or a
+    step over the last quarter of the keys), V by 2^c. A row's maximum then
+    keeps growing as the walk proceeds, by up to a few hundred log2 units, so
+    the fused kernels move their exponent base several times per row, at
+    positions that depend on the shape. a + log2 r <= 8 keeps the logits
+    well conditioned in fp32 (as for the random scales)."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    for _ in range(count):
+        a = int(rng.integers(-4, 5))
+        r = float(2.0 ** rng.uniform(0, 8 - max(a, 0)))
+        cases.append((int(rng.integers(1, 3)), int(rng.integers(1, 3)), int(rng.integers(2, 1500)),
+                      int(rng.choice([64, 128])), bool(rng.integers(0, 2)), a, r, int(rng.integers(-100, 41)),
+                      str(rng.choice(["linear", "square", "late"]))))
+    return cases
+
+
+RISING_LOGITS = rising_logits(30, seed=20261204)
+
+
+def test_rising_logits(fa, oracle_mod):
+    """Seeded random shapes whose logits rise along the key sequence (the
+    exponent-base moves and their tile recomputation at shape-dependent
+    positions), with V scaled from 2^-100 to 2^40. Every kernel, every row
+    against the oracle."""
+    for idx, (B, H, N, D, causal, a, r, c, kind) in enumerate(RISING_LOGITS):
+        q, k, v = oracle_mod.make_inputs(B, H, N, D, seeds={"q": 700 + idx, "k": 800 + idx, "v": 900 + idx})
+        qf, kf, vf = (oracle_mod.bf16_to_f32(x).astype(np.float64) for x in (q, k, v))
+        t = np.arange(N, dtype=np.float64) / max(N - 1, 1)
+        ramp = {"linear": 1 + (r - 1) * t, "square": 1 + (r - 1) * t * t, "late": np.where(t > 0.75, r, 1.0)}[kind]
+        q = oracle_mod.bf16_bits(qf * 2.0 ** a)
+        k = oracle_mod.bf16_bits(kf * ramp[None, None, :, None])
+        v = oracle_mod.bf16_bits(vf * 2.0 ** c)
+        ref = oracle_mod.attention(q, k, v, causal, threads=HOST_THREADS)
+        for kernel in kernels_for(D):
+            say("rising logits", idx, kernel, B, H, N, D, causal, a, round(r, 2), c, kind)
+            acc = oracle_mod.compare(run_bits(fa, kernel, q, k, v, causal), ref)
+            assert acc.passed, f"rising logits {idx} {kernel} {(B, H, N, D, causal, a, r, c, kind)}: {acc}"
